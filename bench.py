@@ -1,0 +1,219 @@
+"""Benchmark of the DSQG hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 2] [--no-cpu-baseline]
+
+A step is one DSQG forward + backward over one batch of the headline workload (config 2:
+B8 H12 N2048 D64, bf16, 44 offsets, synthetic seeded inputs already resident in HBM).  Three
+input sets are rotated so that consecutive steps cannot be served from the 256 MB Infinity Cache.
+Prints one JSON line: tok/s (B*N per step), the roofline of the dominant kernel (algorithmic
+bytes per launch over its average launch time, HIP events on the launch stream), the
+fraction of HBM peak for the whole fwd+bwd step, the ring-buffer decode step (workload 4,
+1000 steps replayed from a HIP graph), and the CPU oracle timed on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+
+
+def _events_ms(fn, reps, stream):
+    import torch
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(reps):
+        fn(i)
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(w, inp_cpu):
+    """CPU oracle (fp32 autograd restatement of the reference) on one sequence of the workload."""
+    import torch
+    from oracle import dsqg_forward_backward
+    b = 0
+    sl = {k: (v[b:b + 1].float() if k in ("q", "k", "v", "dout") else v) for k, v in inp_cpu.items()}
+    threads = torch.get_num_threads()
+
+    def run():
+        dsqg_forward_backward(sl["q"], sl["k"], sl["v"], sl["pos_bias"], sl["dout"],
+                              sl["scale_embed"], w.offsets, sl["score_gain"], sl["if_gain"],
+                              dtype=torch.float32)
+
+    run()  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(w.N / t, 1), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"1 of {w.B} sequences of config {w.index} (H{w.H} N{w.N} D{w.D} "
+                       f"J{w.J}), fwd+bwd, oracle/dsqg_oracle.py fp32 autograd, median of 3 "
+                       f"after 1 warm-up, torch threads={threads}"),
+            "seconds_per_sequence": round(t, 3)}
+
+
+def bench_decode(dev, steps=1000):
+    import torch
+    from dwarf_amd import ops
+    from dwarf_amd.workloads import DECODE, decode_bytes_per_step, make_decode_inputs
+    cfg = DECODE
+    d = make_decode_inputs(device=dev)
+    pos_a = d["pos"].clone()
+    pos_b = torch.empty_like(pos_a)
+    out = torch.empty_like(d["q"])
+    offs = list(cfg["offsets"])
+
+    def step(src, dst):
+        ops.decode_step_into(d["q"], d["k_new"], d["v_new"], d["k_ring"], d["v_ring"], src,
+                             d["pos_bias"], None, None, None, offs, out, dst)
+
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        for i in range(4):
+            step(pos_a, pos_b) if i % 2 == 0 else step(pos_b, pos_a)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for i in range(steps):
+            step(pos_a, pos_b) if i % 2 == 0 else step(pos_b, pos_a)
+    graph.replay()  # warm-up replay
+    torch.cuda.synchronize(dev)
+    st = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    graph.replay()
+    e1.record(st)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / steps
+    nbytes = decode_bytes_per_step(cfg["B"], cfg["H"], cfg["D"], len(offs))
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "decode B256 H12 D64 J44 ring 1537 (config 4)", "steps": steps,
+            "us_per_step": round(us, 3), "tok_per_s": round(cfg["B"] / (us * 1e-6), 1),
+            "algorithmic_bytes_per_step": nbytes, "achieved_GBs": round(gbs, 1),
+            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "timing": "hipGraph replay, HIP events"}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3])
+    ap.add_argument("--sets", type=int, default=3, help="input sets rotated between steps")
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus}, WORLD_SIZE "
+              f"{world} requested). DSQG shards over (batch, head) with no communication; "
+              "multi-GPU runs are not part of this build.", file=sys.stderr)
+        return 2
+
+    import torch
+    from dwarf_amd import ops
+    from dwarf_amd.workloads import WORKLOADS, make_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    w = WORKLOADS[args.config]
+    T = w.B * w.H * w.N
+    E = 2
+    print(f"[bench] config {w.index}: B{w.B} H{w.H} N{w.N} D{w.D} J{w.J} {w.dtype}, "
+          f"{args.sets} input sets, warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
+
+    sets = []
+    for i in range(args.sets):
+        inp = make_inputs(w, device="cpu", seed=w.seed + 100 * i)
+        d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+        fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
+                           d["score_gain"], d["if_gain"], list(w.offsets))
+        bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
+                           d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
+                           d["scale_embed"] is not None, d["score_gain"] is not None,
+                           d["if_gain"] is not None)
+        sets.append((inp if i == 0 else None, d, fl, bl))
+
+    def step(i):
+        _, _, fl, bl = sets[i % len(sets)]
+        fl.run()
+        bl.run()
+
+    stream = torch.cuda.current_stream(dev)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms = _events_ms(step, args.steps, stream)
+    wall = (time.perf_counter() - t0) * 1000.0 / args.steps
+    torch.cuda.synchronize()
+    print(f"[bench] fwd+bwd {ms:.4f} ms/step (wall {wall:.4f})", file=sys.stderr, flush=True)
+
+    # Per-kernel launch durations (each phase launched back to back, rotating the sets).
+    kern = {
+        "dsqg_fwd": (lambda i: sets[i % len(sets)][2].run(), w.fwd_bytes()),
+        "dsqg_bwd_dq": (lambda i: sets[i % len(sets)][3].run("dq"), 5 * T * w.D * E + 8 * T),
+        "dsqg_bwd_dkdv": (lambda i: sets[i % len(sets)][3].run("dkdv"), 6 * T * w.D * E + 8 * T),
+        "dsqg_bwd_params": (lambda i: sets[i % len(sets)][3].run("params"), None),
+    }
+    per = {}
+    for name, (fn, nbytes) in kern.items():
+        fn(0)
+        us = _events_ms(fn, args.steps, stream) * 1000.0
+        per[name] = {"us": round(us, 3)}
+        if nbytes:
+            per[name]["algorithmic_bytes"] = nbytes
+            per[name]["achieved_GBs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+        print(f"[bench] {name}: {us:.2f} us/launch", file=sys.stderr, flush=True)
+    dom = max((k for k in per if "algorithmic_bytes" in per[k]), key=lambda k: per[k]["us"])
+    achieved = per[dom]["achieved_GBs"]
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                "launch_us": per[dom]["us"], "algorithmic_bytes": per[dom]["algorithmic_bytes"]}
+
+    step_bytes = w.fwd_bytes() + w.bwd_bytes()
+    tok_s = w.B * w.N / (ms * 1e-3)
+    result = {
+        "metric": "DSQG fwd+bwd tok/s + % HBM peak (B8 H12 N2048 D64 bf16); decode tok/s",
+        "value": round(tok_s, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)-based inputs per workload spec, 3 rotating sets)",
+        "config": {"workload": f"config {w.index}: DSQG fwd+bwd B{w.B} H{w.H} N{w.N} D{w.D} "
+                               f"J{w.J} bf16", "B": w.B, "H": w.H, "N": w.N, "D": w.D, "J": w.J},
+        "fwd_bwd_algorithmic_bytes": step_bytes,
+        "fwd_bwd_frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": roofline,
+        "kernels": per,
+    }
+    if not args.no_decode:
+        result["decode"] = bench_decode(dev, args.decode_steps)
+        print(f"[bench] decode {result['decode']['us_per_step']} us/step", file=sys.stderr, flush=True)
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle sample ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(w, sets[0][0])
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

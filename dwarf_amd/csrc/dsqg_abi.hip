@@ -1,0 +1,253 @@
+// C ABI of libdsqg_hip.so (declared in include/dsqg.h).  Every entry point validates its
+// arguments on the host before touching HIP, then fills a launch parameter block and
+// dispatches on (dtype, head dim, offset count).  No allocation, no synchronisation, no
+// mutable global state.
+#include <limits.h>
+#include <math.h>
+#include <string.h>
+
+#include "../../include/dsqg.h"
+#include "dsqg_common.hpp"
+#include "dsqg_launch.hpp"
+
+using namespace dsqg;
+
+namespace {
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+size_t elem_size(int dtype) { return dtype == DSQG_F32 ? 4 : 2; }
+
+// Validates the shape block and derives the tap table (dense window W, max offset).
+int check_shape(const dsqg_shape& s, bool need_n, TapTable* taps) {
+  if (s.dtype != DSQG_F32 && s.dtype != DSQG_BF16) return DSQG_EINVAL;
+  if (s.B < 0 || s.H < 0 || s.D <= 0 || (need_n && s.N < 0)) return DSQG_EINVAL;
+  if (s.J < 1 || s.J > DSQG_MAX_OFFSETS) return DSQG_EINVAL;
+  if (s.offsets[0] != 0) return DSQG_EINVAL;
+  for (int j = 1; j < s.J; ++j)
+    if (s.offsets[j] <= s.offsets[j - 1] || s.offsets[j] > (1 << 28)) return DSQG_EINVAL;
+  if (!head_dim_supported(s.D) || s.J > kMaxTaps) return DSQG_EUNSUPPORTED;
+  taps->J = s.J;
+  taps->maxd = s.offsets[s.J - 1];
+  int W = 0;
+  while (W + 1 < s.J && W + 1 <= kMaxWindow && s.offsets[W + 1] == W + 1) ++W;
+  taps->W = W;
+  for (int j = 0; j < kMaxOffsets; ++j) taps->delta[j] = j < s.J ? s.offsets[j] : 0;
+  return DSQG_OK;
+}
+
+// A [B,H,N,D] operand: non-null when non-empty, 16-byte aligned rows, unit D stride,
+// non-negative strides.
+int check_tensor(const void* ptr, const int64_t st[4], int dtype, long long nelem) {
+  if (nelem == 0) return DSQG_OK;
+  if (!ptr || !aligned16(ptr)) return DSQG_EINVAL;
+  if (st[3] != 1) return DSQG_EINVAL;
+  const size_t es = elem_size(dtype);
+  for (int i = 0; i < 3; ++i)
+    if (st[i] < 0 || (st[i] * (int64_t)es) % 16 != 0) return DSQG_EINVAL;
+  return DSQG_OK;
+}
+
+Strides4 to_strides(const int64_t st[4]) { return Strides4{st[0], st[1], st[2], st[3]}; }
+
+int hip_status(hipError_t e) { return e == hipSuccess ? DSQG_OK : DSQG_EHIP; }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct BwdLayout {
+  size_t dpre, part_bias, part_gain, part_if, part_se, total;
+};
+
+BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
+  const dsqg_shape& s = a.shape;
+  const size_t nb = (size_t)s.B * s.H * p.n_chunks;
+  BwdLayout L{};
+  size_t off = 0;
+  L.dpre = off; off = align256(off + sizeof(float) * (size_t)s.B * s.H * s.N);
+  L.part_bias = off; off = align256(off + sizeof(float) * nb * s.J);
+  L.part_gain = off; if (a.dscore_gain) off = align256(off + sizeof(float) * nb * s.J);
+  L.part_if = off; if (a.dif_gain) off = align256(off + sizeof(float) * nb);
+  L.part_se = off; if (a.dscale_embed) off = align256(off + sizeof(float) * nb * s.J * s.D);
+  L.total = off;
+  return L;
+}
+
+int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
+  if (!a) return DSQG_EINVAL;
+  const dsqg_shape& s = a->shape;
+  memset(p, 0, sizeof(*p));
+  int st = check_shape(s, true, &p->taps);
+  if (st) return st;
+  const long long ne = (long long)s.B * s.H * s.N * s.D;
+  if ((st = check_tensor(a->q, a->q_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->k, a->k_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->v, a->v_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->dout, a->dout_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->dq, a->dq_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->dk, a->dk_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->dv, a->dv_stride, s.dtype, ne))) return st;
+  if (ne > 0 && !a->lse) return DSQG_EINVAL;
+  if ((long long)s.J * s.H > 0 && (!a->pos_bias || !a->dpos_bias)) return DSQG_EINVAL;
+  p->B = s.B; p->H = s.H; p->N = s.N;
+  bwd_plan(*p, s.D, a->dscale_embed != nullptr);
+  if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;
+  if ((long long)s.B * s.H * p->n_tiles > INT_MAX / 2) return DSQG_EINVAL;
+  return DSQG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsqg_abi_version(void) { return DSQG_ABI_VERSION; }
+
+const char* dsqg_status_string(int status) {
+  switch (status) {
+    case DSQG_OK: return "ok";
+    case DSQG_EINVAL: return "invalid argument (shape, stride, alignment, pointer or offset table)";
+    case DSQG_EUNSUPPORTED: return "unsupported configuration (no kernel for this head dim)";
+    case DSQG_EHIP: return "HIP launch error";
+    case DSQG_EWORKSPACE: return "workspace missing or too small";
+    default: return "unknown status";
+  }
+}
+
+int dsqg_supported_head_dims(int32_t* dims, int cap) {
+  static const int32_t kDims[] = {32, 64, 128};
+  const int n = (int)(sizeof(kDims) / sizeof(kDims[0]));
+  for (int i = 0; i < n && i < cap; ++i) dims[i] = kDims[i];
+  return n;
+}
+
+int dsqg_fwd(const dsqg_fwd_args* a, dsqg_stream_t stream) {
+  if (!a) return DSQG_EINVAL;
+  const dsqg_shape& s = a->shape;
+  FwdParams p;
+  memset(&p, 0, sizeof(p));
+  int st = check_shape(s, true, &p.taps);
+  if (st) return st;
+  const long long ne = (long long)s.B * s.H * s.N * s.D;
+  if ((st = check_tensor(a->q, a->q_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->k, a->k_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->v, a->v_stride, s.dtype, ne))) return st;
+  if ((st = check_tensor(a->out, a->out_stride, s.dtype, ne))) return st;
+  if ((long long)s.J * s.H > 0 && !a->pos_bias) return DSQG_EINVAL;
+  if ((long long)s.B * s.H * ((s.N + 15) / 16) > INT_MAX / 2) return DSQG_EINVAL;
+  if (ne == 0) return DSQG_OK;
+  p.B = s.B; p.H = s.H; p.N = s.N;
+  p.scale = 1.0f / sqrtf((float)s.D);
+  p.q = a->q; p.qs = to_strides(a->q_stride);
+  p.k = a->k; p.ks = to_strides(a->k_stride);
+  p.v = a->v; p.vs = to_strides(a->v_stride);
+  p.pos_bias = a->pos_bias; p.scale_embed = a->scale_embed;
+  p.score_gain = a->score_gain; p.if_gain = a->if_gain;
+  p.out = a->out; p.os = to_strides(a->out_stride);
+  p.lse = a->lse;
+  return hip_status(launch_fwd(p, s.dtype, s.D, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dsqg_bwd_workspace_size(const dsqg_bwd_args* a, size_t* bytes) {
+  if (!bytes) return DSQG_EINVAL;
+  BwdParams p;
+  int st = check_bwd(a, &p);
+  if (st) return st;
+  *bytes = bwd_layout(*a, p).total;
+  return DSQG_OK;
+}
+
+// Phase selector for the backward entry points.
+enum { kPhaseDq = 1, kPhaseDkdv = 2, kPhaseParams = 4, kPhaseAll = 7 };
+
+static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
+  BwdParams p;
+  int st = check_bwd(a, &p);
+  if (st) return st;
+  const dsqg_shape& s = a->shape;
+  const BwdLayout L = bwd_layout(*a, p);
+  if (L.total > 0) {
+    if (!a->workspace || a->workspace_bytes < L.total) return DSQG_EWORKSPACE;
+    if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return DSQG_EINVAL;
+  }
+  char* ws = static_cast<char*>(a->workspace);
+  p.scale = 1.0f / sqrtf((float)s.D);
+  p.q = a->q; p.qs = to_strides(a->q_stride);
+  p.k = a->k; p.ks = to_strides(a->k_stride);
+  p.v = a->v; p.vs = to_strides(a->v_stride);
+  p.dout = a->dout; p.dos = to_strides(a->dout_stride);
+  p.lse = a->lse;
+  p.pos_bias = a->pos_bias; p.scale_embed = a->scale_embed;
+  p.score_gain = a->score_gain; p.if_gain = a->if_gain;
+  p.dq = a->dq; p.dqs = to_strides(a->dq_stride);
+  p.dk = a->dk; p.dks = to_strides(a->dk_stride);
+  p.dv = a->dv; p.dvs = to_strides(a->dv_stride);
+  p.dpre = reinterpret_cast<float*>(ws + L.dpre);
+  p.part_bias = reinterpret_cast<float*>(ws + L.part_bias);
+  p.part_gain = a->dscore_gain ? reinterpret_cast<float*>(ws + L.part_gain) : nullptr;
+  p.part_if = a->dif_gain ? reinterpret_cast<float*>(ws + L.part_if) : nullptr;
+  p.part_se = a->dscale_embed ? reinterpret_cast<float*>(ws + L.part_se) : nullptr;
+
+  hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  const bool rows = (long long)s.B * s.H * s.N > 0;
+  if ((phases & kPhaseDq) && rows) {
+    const unsigned nb = (unsigned)((long long)s.B * s.H * p.n_chunks);
+    if ((st = hip_status(launch_bwd_dq(p, s.dtype, s.D, nb, hs)))) return st;
+  }
+  if ((phases & kPhaseDkdv) && rows) {
+    const unsigned nb = (unsigned)((long long)s.B * s.H * p.n_tiles);
+    if ((st = hip_status(launch_bwd_dkdv(p, s.dtype, s.D, nb, hs)))) return st;
+  }
+  if (phases & kPhaseParams) {
+    ReduceParams r;
+    r.B = s.B; r.H = s.H; r.J = s.J; r.D = s.D;
+    r.n_chunks = rows ? p.n_chunks : 0;  // no rows: the empty sums write zeros
+    r.part_bias = p.part_bias; r.part_se = p.part_se;
+    r.part_gain = p.part_gain; r.part_if = p.part_if;
+    r.dpos_bias = a->dpos_bias; r.dscale_embed = a->dscale_embed;
+    r.dscore_gain = a->dscore_gain; r.dif_gain = a->dif_gain;
+    if ((st = hip_status(launch_bwd_reduce(r, hs)))) return st;
+  }
+  return DSQG_OK;
+}
+
+int dsqg_bwd(const dsqg_bwd_args* a, dsqg_stream_t stream) { return run_bwd(a, kPhaseAll, stream); }
+int dsqg_bwd_dq(const dsqg_bwd_args* a, dsqg_stream_t stream) { return run_bwd(a, kPhaseDq, stream); }
+int dsqg_bwd_dkdv(const dsqg_bwd_args* a, dsqg_stream_t stream) {
+  return run_bwd(a, kPhaseDkdv, stream);
+}
+int dsqg_bwd_params(const dsqg_bwd_args* a, dsqg_stream_t stream) {
+  return run_bwd(a, kPhaseParams, stream);
+}
+
+int dsqg_decode_step(const dsqg_decode_args* a, dsqg_stream_t stream) {
+  if (!a) return DSQG_EINVAL;
+  const dsqg_shape& s = a->shape;
+  DecodeParams p;
+  memset(&p, 0, sizeof(p));
+  int st = check_shape(s, false, &p.taps);
+  if (st) return st;
+  if (a->S <= p.taps.maxd) return DSQG_EINVAL;
+  const long long rows = (long long)s.B * s.H;
+  if (rows == 0) return DSQG_OK;
+  const void* ptrs[] = {a->q, a->k_new, a->v_new, a->k_ring, a->v_ring, a->out};
+  for (const void* ptr : ptrs)
+    if (!ptr || !aligned16(ptr)) return DSQG_EINVAL;
+  if (!a->pos || !a->pos_bias) return DSQG_EINVAL;
+  if (a->pos_next && a->pos_next == a->pos) return DSQG_EINVAL;
+  if (rows > INT_MAX) return DSQG_EINVAL;
+  p.B = s.B; p.H = s.H; p.S = a->S;
+  p.scale = 1.0f / sqrtf((float)s.D);
+  p.q = a->q; p.k_new = a->k_new; p.v_new = a->v_new;
+  p.k_ring = a->k_ring; p.v_ring = a->v_ring;
+  p.pos = reinterpret_cast<const long long*>(a->pos);
+  p.pos_next = reinterpret_cast<long long*>(a->pos_next);
+  p.pos_bias = a->pos_bias; p.scale_embed = a->scale_embed;
+  p.score_gain = a->score_gain; p.if_gain = a->if_gain;
+  p.out = a->out;
+  return hip_status(launch_decode(p, s.dtype, s.D, reinterpret_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"
+
+namespace dsqg {
+bool head_dim_supported(int D) { return D == 32 || D == 64 || D == 128; }
+}  // namespace dsqg

@@ -1,0 +1,23 @@
+// Internal launchers shared between the kernel files and the C ABI (dsqg_abi.hip).
+#pragma once
+
+#include "dsqg_common.hpp"
+
+namespace dsqg {
+
+// dtype: 0 = f32, 1 = bf16.  Each returns hipGetLastError() after its launches, or
+// hipErrorInvalidValue for a head dim without a kernel (the ABI checks that first).
+hipError_t launch_fwd(const FwdParams& p, int dtype, int D, hipStream_t st);
+
+// Tiling of the backward for these sizes; fills n_tiles / tiles_per_block / n_chunks.
+// With se_grad the dq workgroups cover more rows each, so fewer [J,D] partials are written.
+void bwd_plan(BwdParams& p, int D, bool se_grad);
+hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st);
+hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
+hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
+
+hipError_t launch_decode(const DecodeParams& p, int dtype, int D, hipStream_t st);
+
+bool head_dim_supported(int D);
+
+}  // namespace dsqg

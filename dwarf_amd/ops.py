@@ -1,0 +1,290 @@
+"""torch custom ops over the C ABI: ``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::dsqg_decode``.
+
+The ops take device tensors, pass raw pointers, element strides and the current HIP stream
+to libdsqg_hip.so through ctypes, and allocate their outputs (and the backward workspace) with
+torch's caching allocator.  ``dwarf::dsqg_fwd`` carries an autograd formula that calls
+``dwarf::dsqg_bwd``, and every op has a fake (meta) implementation so graphs can be traced.
+
+Tensors must live on a ROCm GPU: there is no CPU path, and a missing library raises.
+
+Reference counterparts: _DSQGFnV3.forward / .backward (kernels/dsqg_attention_v3.py:359-442).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.DSQG_F32, torch.bfloat16: _lib.DSQG_BF16}
+
+
+def _ptr(t: Optional[Tensor]):
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _require_gpu(*ts: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"dwarf_amd DSQG ops need tensors on a ROCm GPU, got device {t.device}; "
+                "there is no CPU implementation")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _rows_ready(t: Tensor) -> Tensor:
+    """Keep t if the kernels can read it in place (unit inner stride, 16-byte aligned rows)."""
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all(s >= 0 and (s * es) % 16 == 0 for s in t.stride()[:-1]))
+    return t if ok or t.numel() == 0 else t.contiguous()
+
+
+def _param(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.detach().to(torch.float32).contiguous()
+
+
+def _strides(t: Tensor):
+    return (ctypes.c_int64 * 4)(*t.stride())
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+# ------------------------------------------------------------------------------------------
+# Forward
+# ------------------------------------------------------------------------------------------
+
+class FwdLaunch:
+    """Argument block and outputs of one forward call, reusable: ``run()`` relaunches it."""
+
+    def __init__(self, q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
+        dev = _require_gpu(q, k, v, pos_bias, scale_embed, score_gain, if_gain)
+        self.lib = _lib.load()
+        self.device = dev
+        B, H, N, D = q.shape
+        code = _DTYPE_CODE.get(q.dtype)
+        if code is None or k.dtype != q.dtype or v.dtype != q.dtype:
+            raise AssertionError(f"q/k/v must share dtype float32 or bfloat16, got "
+                                 f"{q.dtype}/{k.dtype}/{v.dtype}")
+        q, k, v = _rows_ready(q), _rows_ready(k), _rows_ready(v)
+        pb, se, sg, ig = _param(pos_bias), _param(scale_embed), _param(score_gain), _param(if_gain)
+        self.out = torch.empty((B, H, N, D), dtype=q.dtype, device=dev)
+        self.lse = torch.empty((B, H, N), dtype=torch.float32, device=dev)
+        self._keep = (q, k, v, pb, se, sg, ig)
+        a = _lib.FwdArgs()
+        a.shape = _lib.make_shape(code, B, H, N, D, offsets)
+        a.q, a.q_stride = _ptr(q), _strides(q)
+        a.k, a.k_stride = _ptr(k), _strides(k)
+        a.v, a.v_stride = _ptr(v), _strides(v)
+        a.pos_bias, a.scale_embed, a.score_gain, a.if_gain = _ptr(pb), _ptr(se), _ptr(sg), _ptr(ig)
+        a.out, a.out_stride = _ptr(self.out), _strides(self.out)
+        a.lse = _ptr(self.lse)
+        self.args = a
+
+    def run(self) -> None:
+        _lib.check(self.lib.dsqg_fwd(ctypes.byref(self.args), _stream(self.device)), "dsqg_fwd")
+
+
+@torch.library.custom_op("dwarf::dsqg_fwd", mutates_args=())
+def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
+             scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
+             if_gain: Optional[Tensor], offsets: List[int]) -> Tuple[Tensor, Tensor]:
+    """out [B,H,N,D] (dtype of q) and lse [B,H,N] fp32."""
+    launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
+    launch.run()
+    return launch.out, launch.lse
+
+
+@dsqg_fwd.register_fake
+def _(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
+    B, H, N, D = q.shape
+    return q.new_empty((B, H, N, D)), q.new_empty((B, H, N), dtype=torch.float32)
+
+
+# ------------------------------------------------------------------------------------------
+# Backward
+# ------------------------------------------------------------------------------------------
+
+class BwdLaunch:
+    """Argument block, outputs and workspace of one backward call.
+
+    ``run()`` launches all three phases (dsqg_bwd); ``run("dq")``, ``run("dkdv")`` and
+    ``run("params")`` launch one phase each (dsqg_bwd_dq / _dkdv / _params), in that order.
+    """
+
+    _ENTRY = {None: "dsqg_bwd", "dq": "dsqg_bwd_dq", "dkdv": "dsqg_bwd_dkdv",
+              "params": "dsqg_bwd_params"}
+
+    def __init__(self, q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
+                 need_dse, need_dg, need_da):
+        dev = _require_gpu(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain)
+        self.lib = _lib.load()
+        self.device = dev
+        B, H, N, D = q.shape
+        J = len(offsets)
+        code = _DTYPE_CODE.get(q.dtype)
+        if code is None or dout.dtype != q.dtype:
+            raise AssertionError(f"q and dout must share dtype float32 or bfloat16, got "
+                                 f"{q.dtype}/{dout.dtype}")
+        q, k, v, dout = _rows_ready(q), _rows_ready(k), _rows_ready(v), _rows_ready(dout)
+        lse = lse.contiguous()
+        pb, se, sg, ig = _param(pos_bias), _param(scale_embed), _param(score_gain), _param(if_gain)
+        self.dq = torch.empty((B, H, N, D), dtype=q.dtype, device=dev)
+        self.dk = torch.empty_like(self.dq)
+        self.dv = torch.empty_like(self.dq)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.dpos_bias = torch.empty((J, H), **f32)
+        self.dscale_embed = torch.empty((J, D) if need_dse else (0,), **f32)
+        self.dscore_gain = torch.empty((H, J) if need_dg else (0,), **f32)
+        self.dif_gain = torch.empty((H,) if need_da else (0,), **f32)
+        self._keep = (q, k, v, dout, lse, pb, se, sg, ig)
+        a = _lib.BwdArgs()
+        a.shape = _lib.make_shape(code, B, H, N, D, offsets)
+        a.q, a.q_stride = _ptr(q), _strides(q)
+        a.k, a.k_stride = _ptr(k), _strides(k)
+        a.v, a.v_stride = _ptr(v), _strides(v)
+        a.dout, a.dout_stride = _ptr(dout), _strides(dout)
+        a.lse = _ptr(lse)
+        a.pos_bias, a.scale_embed, a.score_gain, a.if_gain = _ptr(pb), _ptr(se), _ptr(sg), _ptr(ig)
+        a.dq, a.dq_stride = _ptr(self.dq), _strides(self.dq)
+        a.dk, a.dk_stride = _ptr(self.dk), _strides(self.dk)
+        a.dv, a.dv_stride = _ptr(self.dv), _strides(self.dv)
+        a.dpos_bias = _ptr(self.dpos_bias)
+        a.dscale_embed = _ptr(self.dscale_embed) if need_dse else None
+        a.dscore_gain = _ptr(self.dscore_gain) if need_dg else None
+        a.dif_gain = _ptr(self.dif_gain) if need_da else None
+        nbytes = ctypes.c_size_t(0)
+        _lib.check(self.lib.dsqg_bwd_workspace_size(ctypes.byref(a), ctypes.byref(nbytes)),
+                   "dsqg_bwd_workspace_size")
+        self.workspace = torch.empty((max(int(nbytes.value), 1),), dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = self.workspace.data_ptr(), int(nbytes.value)
+        self.args = a
+
+    def run(self, phase: Optional[str] = None) -> None:
+        name = self._ENTRY[phase]
+        _lib.check(getattr(self.lib, name)(ctypes.byref(self.args), _stream(self.device)), name)
+
+    def outputs(self):
+        return (self.dq, self.dk, self.dv, self.dpos_bias, self.dscale_embed, self.dscore_gain,
+                self.dif_gain)
+
+
+@torch.library.custom_op("dwarf::dsqg_bwd", mutates_args=())
+def dsqg_bwd(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, lse: Tensor, pos_bias: Tensor,
+             scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
+             if_gain: Optional[Tensor], offsets: List[int], need_dse: bool, need_dg: bool,
+             need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dq, dk, dv, dpos_bias, dscale_embed, dscore_gain, dif_gain); unrequested ones are empty."""
+    launch = BwdLaunch(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
+                       need_dse, need_dg, need_da)
+    launch.run()
+    return launch.outputs()
+
+
+@dsqg_bwd.register_fake
+def _(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets, need_dse,
+      need_dg, need_da):
+    B, H, N, D = q.shape
+    J = len(offsets)
+    f = dict(dtype=torch.float32)
+    return (q.new_empty(q.shape), q.new_empty(q.shape), q.new_empty(q.shape),
+            q.new_empty((J, H), **f), q.new_empty((J, D) if need_dse else (0,), **f),
+            q.new_empty((H, J) if need_dg else (0,), **f), q.new_empty((H,) if need_da else (0,), **f))
+
+
+def _setup_context(ctx, inputs, output):
+    q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets = inputs
+    _, lse = output
+    ctx.save_for_backward(q, k, v, lse, pos_bias, scale_embed, score_gain, if_gain)
+    ctx.offsets = list(offsets)
+    ctx.mark_non_differentiable(lse)
+
+
+def _backward(ctx, dout, _dlse):
+    q, k, v, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    need_dse = bool(need[4]) and scale_embed is not None
+    need_dg = bool(need[5]) and score_gain is not None
+    need_da = bool(need[6]) and if_gain is not None
+    dq, dk, dv, dpb, dse, dg, da = dsqg_bwd(
+        q, k, v, dout.to(q.dtype), lse, pos_bias, scale_embed, score_gain, if_gain,
+        ctx.offsets, need_dse, need_dg, need_da)
+    return (dq, dk, dv, dpb.to(pos_bias.dtype),
+            dse.to(scale_embed.dtype) if need_dse else None,
+            dg.to(score_gain.dtype) if need_dg else None,
+            da.to(if_gain.dtype) if need_da else None, None)
+
+
+torch.library.register_autograd("dwarf::dsqg_fwd", _backward, setup_context=_setup_context)
+
+
+# ------------------------------------------------------------------------------------------
+# Decode step
+# ------------------------------------------------------------------------------------------
+
+@torch.library.custom_op("dwarf::dsqg_decode", mutates_args=("k_ring", "v_ring"))
+def dsqg_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: Tensor,
+                pos: Tensor, pos_bias: Tensor, scale_embed: Optional[Tensor],
+                score_gain: Optional[Tensor], if_gain: Optional[Tensor],
+                offsets: List[int]) -> Tensor:
+    """One ring-buffer decode step; writes k_new/v_new into the rings, returns out [B,H,D]."""
+    out = torch.empty_like(q)
+    decode_step_into(q, k_new, v_new, k_ring, v_ring, pos, pos_bias, scale_embed, score_gain,
+                     if_gain, offsets, out, None)
+    return out
+
+
+@dsqg_decode.register_fake
+def _(q, k_new, v_new, k_ring, v_ring, pos, pos_bias, scale_embed, score_gain, if_gain, offsets):
+    return torch.empty_like(q)
+
+
+def decode_step_into(q, k_new, v_new, k_ring, v_ring, pos, pos_bias, scale_embed, score_gain,
+                     if_gain, offsets, out, pos_next=None) -> None:
+    """Decode step writing into a caller-provided ``out`` (and ``pos_next`` = pos + 1 if given).
+
+    Every tensor must already be contiguous on the GPU and parameters fp32, so the call
+    allocates nothing and can be captured in a HIP graph.
+    """
+    dev = _require_gpu(q, k_new, v_new, k_ring, v_ring, pos, pos_bias, out)
+    lib = _lib.load()
+    B, H, S, D = k_ring.shape
+    code = _DTYPE_CODE.get(q.dtype)
+    if code is None or any(t.dtype != q.dtype for t in (k_new, v_new, k_ring, v_ring, out)):
+        raise AssertionError("q, k_new, v_new, rings and out must share dtype float32 or bfloat16")
+    for name, t, shp in (("q", q, (B, H, D)), ("k_new", k_new, (B, H, D)),
+                         ("v_new", v_new, (B, H, D)), ("v_ring", v_ring, (B, H, S, D)),
+                         ("out", out, (B, H, D))):
+        if tuple(t.shape) != shp or not t.is_contiguous():
+            raise AssertionError(f"{name} must be a contiguous {shp} tensor, got "
+                                 f"{tuple(t.shape)} (contiguous={t.is_contiguous()})")
+    if not k_ring.is_contiguous():
+        raise AssertionError("k_ring must be contiguous")
+    if pos.dtype != torch.int64 or tuple(pos.shape) != (B,) or not pos.is_contiguous():
+        raise AssertionError("pos must be a contiguous int64 [B] tensor")
+    params = [pos_bias, scale_embed, score_gain, if_gain]
+    for t in params:
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise AssertionError("pos_bias/scale_embed/score_gain/if_gain must be contiguous fp32")
+    a = _lib.DecodeArgs()
+    a.shape = _lib.make_shape(code, B, H, 0, D, offsets)
+    a.S = S
+    a.q, a.k_new, a.v_new = _ptr(q), _ptr(k_new), _ptr(v_new)
+    a.k_ring, a.v_ring = _ptr(k_ring), _ptr(v_ring)
+    a.pos, a.pos_next = _ptr(pos), _ptr(pos_next)
+    a.pos_bias, a.scale_embed, a.score_gain, a.if_gain = (_ptr(t) for t in params)
+    a.out = _ptr(out)
+    _lib.check(lib.dsqg_decode_step(ctypes.byref(a), _stream(dev)), "dsqg_decode_step")

@@ -1,0 +1,133 @@
+"""GPU parity of the ring-buffer decode step (workload 4) against the CPU oracle.
+
+Tolerance: bf16 outputs vs the fp32 oracle on the same bf16 inputs, max|x - ref| <= 2e-2 *
+max(1, max|ref|); fp32 outputs vs the float64 oracle, <= 1e-5 * max|ref|.  Ring contents are
+compared bit for bit (the step copies rows).
+"""
+
+import pytest
+import torch
+
+import dwarf_amd
+from dwarf_amd import ops
+from dwarf_amd.offsets import OFFSETS_V3
+from dwarf_amd.workloads import DECODE, make_decode_inputs
+from oracle import decode_step, dsqg_forward
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[decode] {msg}", flush=True)
+
+
+def _err(got, ref):
+    return (got.double() - ref.double()).abs().max().item(), ref.abs().max().item()
+
+
+def test_decode_workload_1000_steps(gpu_device):
+    """Workload 4: B256 H12 D64, 1537-slot rings, positions from [1536, 8191], 1000 steps,
+    every step checked against the oracle's gather over its own copy of the rings."""
+    cfg = DECODE
+    inp = make_decode_inputs()
+    d = {k: v.to(gpu_device) for k, v in inp.items()}
+    k_ring_ref, v_ring_ref = inp["k_ring"].clone(), inp["v_ring"].clone()
+    pos = inp["pos"].clone()
+    B, H, D = cfg["B"], cfg["H"], cfg["D"]
+    g = torch.Generator().manual_seed(77)
+    worst = 0.0
+    steps = cfg["steps"]
+    for step in range(steps):
+        q, kn, vn = (torch.randn(B, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+        out = ops.dsqg_decode(q.to(gpu_device), kn.to(gpu_device), vn.to(gpu_device),
+                              d["k_ring"], d["v_ring"], pos.to(gpu_device), d["pos_bias"],
+                              None, None, None, list(OFFSETS_V3)).cpu()
+        ref = decode_step(q.float(), kn.float(), vn.float(), k_ring_ref, v_ring_ref, pos,
+                          inp["pos_bias"])
+        err, scale = _err(out, ref)
+        worst = max(worst, err)
+        assert err <= 2e-2 * max(1.0, scale), f"step {step}: err {err:.3e}"
+        pos = pos + 1
+        if step % 200 == 0:
+            _say(f"step {step} err {err:.3e}")
+    _say(f"{steps} steps, worst err {worst:.3e}")
+    assert torch.equal(d["k_ring"].cpu(), k_ring_ref)
+    assert torch.equal(d["v_ring"].cpu(), v_ring_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("p", [0, 7, 40, 1535, 1536, 2500])
+def test_decode_equals_full_sequence_row(gpu_device, dtype, p):
+    """After prefilling the ring from a sequence of length p, the step at position p equals
+    row p of the full-sequence forward (taps with p - delta < 0 are masked, not wrapped)."""
+    B, H, D = 3, 2, 64
+    g = torch.Generator().manual_seed(1000 + p)
+    qs, ks, vs = (torch.randn(B, H, p + 1, D, generator=g).to(dtype) for _ in range(3))
+    pb = torch.randn(44, H, generator=g) * 0.5
+    se = torch.randn(44, D, generator=g) * 0.1
+    sg = torch.rand(H, 44, generator=g) + 0.5
+    a = torch.rand(H, generator=g) * 0.4 + 0.8
+    cache = dwarf_amd.DSQGRingCache(B, H, D, OFFSETS_V3, dtype=dtype, device=gpu_device)
+    if p > 0:
+        cache.prefill(ks[:, :, :p].to(gpu_device), vs[:, :, :p].to(gpu_device))
+    else:
+        cache.pos.zero_()
+    dev = {n: t.to(gpu_device) for n, t in (("pb", pb), ("se", se), ("sg", sg), ("a", a))}
+    out = cache.step(qs[:, :, p].to(gpu_device), ks[:, :, p].to(gpu_device),
+                     vs[:, :, p].to(gpu_device), dev["pb"], dev["se"], dev["sg"], dev["a"]).cpu()
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref = dsqg_forward(qs.to(cd), ks.to(cd), vs.to(cd), pb.to(cd), se.to(cd), OFFSETS_V3,
+                       sg.to(cd), a.to(cd))[:, :, p]
+    err, scale = _err(out, ref)
+    bound = 1e-5 * scale if dtype == torch.float32 else 2e-2 * max(1.0, scale)
+    _say(f"p={p} {dtype}: err {err:.3e} bound {bound:.3e}")
+    assert err <= bound
+    assert int(cache.pos[0]) == p + 1
+
+
+def test_decode_pos_next_and_graph_replay(gpu_device):
+    """A captured step with pos/pos_next ping-pong replays correctly several times in a row."""
+    B, H, D, S = 8, 4, 64, 1537
+    inp = make_decode_inputs(B=B, H=H, D=D, S=S, seed=5)
+    d = {k: v.to(gpu_device) for k, v in inp.items()}
+    k_ref, v_ref = inp["k_ring"].clone(), inp["v_ring"].clone()
+    pos_a = d["pos"].clone()
+    pos_b = torch.empty_like(pos_a)
+    out = torch.empty_like(d["q"])
+    offs = list(OFFSETS_V3)
+    pb = d["pos_bias"]
+
+    def step(src, dst):
+        ops.decode_step_into(d["q"], d["k_new"], d["v_new"], d["k_ring"], d["v_ring"], src, pb,
+                             None, None, None, offs, out, dst)
+
+    s = torch.cuda.Stream(gpu_device)
+    s.wait_stream(torch.cuda.current_stream(gpu_device))
+    with torch.cuda.stream(s):       # warm-up outside the graph (also checks pos_next)
+        step(pos_a, pos_b)
+    torch.cuda.current_stream(gpu_device).wait_stream(s)
+    torch.cuda.synchronize(gpu_device)
+    pos = inp["pos"].clone()
+    ref = decode_step(inp["q"].float(), inp["k_new"].float(), inp["v_new"].float(), k_ref, v_ref,
+                      pos, inp["pos_bias"])
+    assert torch.equal(pos_b.cpu(), pos + 1)
+    err, scale = _err(out.cpu(), ref)
+    assert err <= 2e-2 * max(1.0, scale)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        step(pos_b, pos_a)
+        step(pos_a, pos_b)
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize(gpu_device)
+        for _ in range(2):
+            pos = pos + 1
+            ref = decode_step(inp["q"].float(), inp["k_new"].float(), inp["v_new"].float(), k_ref,
+                              v_ref, pos, inp["pos_bias"])
+        # the graph's second step is the last one; out holds its result
+        err, scale = _err(out.cpu(), ref)
+        _say(f"replay {rep}: err {err:.3e}")
+        assert err <= 2e-2 * max(1.0, scale)
+        assert torch.equal(pos_b.cpu(), pos + 1)
+    assert torch.equal(d["k_ring"].cpu(), k_ref) and torch.equal(d["v_ring"].cpu(), v_ref)

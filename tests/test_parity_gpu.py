@@ -1,0 +1,249 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle on the same inputs.
+
+Tolerances (written here, checked per tensor):
+  * fp32 kernels vs the float64 oracle:  max|x - ref| <= 1e-5 * max|ref|.
+  * bf16 kernels vs the fp32 oracle fed the same bf16-rounded inputs:
+        max|x - ref| <= 2e-2 * max(1, max|ref|)
+    i.e. 2e-2 absolute on unit-scale tensors; on tensors whose entries exceed 1 (gradients at
+    N(0,1) inputs reach |dq| ~ 10) the bound scales with the tensor, since storing such values
+    in bf16 alone costs 2^-9 * |x|.
+Masking (n - delta < 0) is exercised at every N below max(delta) and by rows 0..1535 of the
+full-size configs.
+"""
+
+import math
+
+import pytest
+import torch
+
+import dwarf_amd
+from dwarf_amd import ops
+from dwarf_amd.offsets import OFFSETS_J46, OFFSETS_J47, OFFSETS_V3
+from dwarf_amd.workloads import WORKLOADS, make_inputs
+from oracle import dsqg_forward, dsqg_forward_backward
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[parity] {msg}", flush=True)
+
+
+def oracle_chunked(inp, offsets, dtype, backward=True):
+    """Oracle over batch chunks (elementwise identical to one call; parameter grads summed)."""
+    B = inp["q"].shape[0]
+    outs = {}
+    for b in range(B):
+        sl = {k: (v[b:b + 1] if k in ("q", "k", "v", "dout") else v) for k, v in inp.items()}
+        if backward:
+            r = dsqg_forward_backward(sl["q"], sl["k"], sl["v"], sl["pos_bias"], sl["dout"],
+                                      sl.get("scale_embed"), offsets, sl.get("score_gain"),
+                                      sl.get("if_gain"), dtype=dtype)
+        else:
+            o, l = dsqg_forward(*(None if t is None else t.to(dtype) for t in
+                                  (sl["q"], sl["k"], sl["v"], sl["pos_bias"], sl.get("scale_embed"))),
+                                offsets=offsets,
+                                score_gain=None if sl.get("score_gain") is None else sl["score_gain"].to(dtype),
+                                if_gain=None if sl.get("if_gain") is None else sl["if_gain"].to(dtype),
+                                return_lse=True)
+            r = {"out": o, "lse": l}
+        for key, val in r.items():
+            if key in ("out", "lse", "dq", "dk", "dv"):
+                outs.setdefault(key, []).append(val)
+            else:
+                outs[key] = outs[key] + val if key in outs else val
+    return {k: (torch.cat(v, 0) if isinstance(v, list) else v) for k, v in outs.items()}
+
+
+def gpu_run(inp, offsets, dev, backward=True):
+    d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+    out, lse = ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], d.get("scale_embed"),
+                            d.get("score_gain"), d.get("if_gain"), list(offsets))
+    res = {"out": out, "lse": lse}
+    if backward:
+        dq, dk, dv, dpb, dse, dg, da = ops.dsqg_bwd(
+            d["q"], d["k"], d["v"], d["dout"], lse, d["pos_bias"], d.get("scale_embed"),
+            d.get("score_gain"), d.get("if_gain"), list(offsets),
+            d.get("scale_embed") is not None, d.get("score_gain") is not None,
+            d.get("if_gain") is not None)
+        res.update(dq=dq, dk=dk, dv=dv, dpos_bias=dpb)
+        if d.get("scale_embed") is not None:
+            res["dscale_embed"] = dse
+        if d.get("score_gain") is not None:
+            res["dscore_gain"] = dg
+        if d.get("if_gain") is not None:
+            res["dif_gain"] = da
+    torch.cuda.synchronize(dev)
+    return {k: v.cpu() for k, v in res.items()}
+
+
+def check(name, got, ref, mode):
+    got, ref = got.double(), ref.double()
+    assert got.shape == ref.shape, f"{name}: shape {tuple(got.shape)} vs {tuple(ref.shape)}"
+    assert torch.isfinite(got).all(), f"{name}: non-finite values"
+    err = (got - ref).abs().max().item() if ref.numel() else 0.0
+    scale = ref.abs().max().item() if ref.numel() else 0.0
+    if mode == "fp32":
+        bound = 1e-5 * scale
+    else:
+        bound = 2e-2 * max(1.0, scale)
+    _say(f"{name}: max err {err:.3e} (bound {bound:.3e}, max|ref| {scale:.3e})")
+    assert err <= bound, f"{name}: max err {err:.3e} > {bound:.3e}"
+
+
+def compare(got, ref, mode, keys=None):
+    for key in keys or ref.keys():
+        if key in got:
+            check(key, got[key], ref[key], mode)
+
+
+def _rand_inputs(B, H, N, D, offsets, dtype, seed, se=True, gains=True):
+    g = torch.Generator().manual_seed(seed)
+    J = len(offsets)
+    shp = (B, H, N, D)
+    inp = dict(q=torch.randn(shp, generator=g), k=torch.randn(shp, generator=g),
+               v=torch.randn(shp, generator=g), dout=torch.randn(shp, generator=g),
+               pos_bias=torch.randn(J, H, generator=g) * 0.5,
+               scale_embed=torch.randn(J, D, generator=g) * 0.1 if se else None,
+               score_gain=torch.rand(H, J, generator=g) + 0.5 if gains else None,
+               if_gain=torch.rand(H, generator=g) * 0.4 + 0.8 if gains else None)
+    for k in ("q", "k", "v", "dout"):
+        inp[k] = inp[k].to(dtype)
+    return inp
+
+
+# ---------------------------------------------------------------------------------------------
+# Workload configurations
+# ---------------------------------------------------------------------------------------------
+
+def test_config0_fp32_forward(gpu_device):
+    w = WORKLOADS[0]
+    inp = make_inputs(w)
+    _say("config 0 fp32 forward B1 H8 N2048 D32")
+    got = gpu_run(inp, w.offsets, gpu_device, backward=False)
+    ref = oracle_chunked(inp, w.offsets, torch.float64, backward=False)
+    compare(got, ref, "fp32")
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_fp32_fwd_bwd_all_parameters(gpu_device, D):
+    inp = _rand_inputs(2, 3, 1700, D, OFFSETS_V3, torch.float32, seed=100 + D)
+    _say(f"fp32 fwd+bwd B2 H3 N1700 D{D} with se, g, a")
+    got = gpu_run(inp, OFFSETS_V3, gpu_device)
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float64)
+    compare(got, ref, "fp32")
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_bf16_workload_fwd_bwd(gpu_device, cfg):
+    w = WORKLOADS[cfg]
+    inp = make_inputs(w)
+    _say(f"config {cfg} bf16 fwd+bwd B{w.B} H{w.H} N{w.N} D{w.D} J{w.J}")
+    got = gpu_run(inp, w.offsets, gpu_device)
+    ref = oracle_chunked(inp, w.offsets, torch.float32)
+    compare(got, ref, "bf16")
+    # sum_j dbias[j,h] = 0 (each row's dS sums to zero over its taps)
+    assert got["dpos_bias"].sum(0).abs().max().item() <= 1e-3 * max(1.0, got["dpos_bias"].abs().max().item())
+
+
+# ---------------------------------------------------------------------------------------------
+# Edge cases
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("N", [1, 2, 31, 33, 47, 49, 65, 129, 257, 1535, 1537, 2047])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ragged_sequence_lengths(gpu_device, N, dtype):
+    inp = _rand_inputs(1, 2, N, 64, OFFSETS_V3, dtype, seed=N)
+    _say(f"ragged N={N} {dtype}")
+    got = gpu_run(inp, OFFSETS_V3, gpu_device)
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float64 if dtype == torch.float32 else torch.float32)
+    compare(got, ref, "fp32" if dtype == torch.float32 else "bf16")
+
+
+@pytest.mark.parametrize("offsets,N", [(OFFSETS_J47, 4097), (OFFSETS_J46, 3100),
+                                       ((0, 1, 2, 5, 9, 100), 300), ((0,), 40),
+                                       (tuple(range(48)), 200)])
+def test_other_offset_tables(gpu_device, offsets, N):
+    inp = _rand_inputs(1, 2, N, 32, offsets, torch.float32, seed=len(offsets))
+    _say(f"offsets J={len(offsets)} N={N}")
+    got = gpu_run(inp, offsets, gpu_device)
+    ref = oracle_chunked(inp, offsets, torch.float64)
+    compare(got, ref, "fp32")
+
+
+def test_empty_inputs(gpu_device):
+    for shape in ((0, 2, 16, 64), (1, 2, 0, 64)):
+        inp = _rand_inputs(*shape, OFFSETS_V3, torch.bfloat16, seed=1)
+        got = gpu_run(inp, OFFSETS_V3, gpu_device)
+        assert got["out"].shape == shape and got["dq"].shape == shape
+        assert (got["dpos_bias"] == 0).all() and (got["dscale_embed"] == 0).all()
+
+
+def test_strided_views_match_contiguous(gpu_device):
+    """q/k/v as head-split views of one [B,N,3*H*D] projection (no permute copies)."""
+    B, H, N, D = 2, 4, 600, 64
+    g = torch.Generator().manual_seed(5)
+    qkv = torch.randn(B, N, 3 * H * D, generator=g).to(torch.bfloat16).to(gpu_device)
+    q, k, v = (t.view(B, N, H, D).permute(0, 2, 1, 3) for t in qkv.split(H * D, dim=-1))
+    pb = (torch.randn(44, H, generator=g) * 0.5).to(gpu_device)
+    se = (torch.randn(44, D, generator=g) * 0.1).to(gpu_device)
+    o1, l1 = ops.dsqg_fwd(q, k, v, pb, se, None, None, list(OFFSETS_V3))
+    o2, l2 = ops.dsqg_fwd(q.contiguous(), k.contiguous(), v.contiguous(), pb, se, None, None,
+                          list(OFFSETS_V3))
+    assert q.stride(2) == 3 * H * D
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+def test_backward_is_deterministic(gpu_device):
+    inp = _rand_inputs(4, 8, 2048, 64, OFFSETS_V3, torch.bfloat16, seed=9)
+    a = gpu_run(inp, OFFSETS_V3, gpu_device)
+    b = gpu_run(inp, OFFSETS_V3, gpu_device)
+    for key in a:
+        assert torch.equal(a[key], b[key]), key
+
+
+# ---------------------------------------------------------------------------------------------
+# Public API (autograd, dtype rules, reference aliases)
+# ---------------------------------------------------------------------------------------------
+
+def test_autograd_api_matches_oracle(gpu_device):
+    inp = _rand_inputs(2, 4, 700, 32, OFFSETS_V3, torch.bfloat16, seed=21, gains=False)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    q, k, v = (d[n].clone().requires_grad_(True) for n in ("q", "k", "v"))
+    pb = d["pos_bias"].clone().requires_grad_(True)
+    se = d["scale_embed"].clone().requires_grad_(True)
+    out = dwarf_amd.dsqg_attention_v3(q, k, v, pb, se)
+    out.backward(d["dout"])
+    got = {"out": out.detach().cpu(), "dq": q.grad.cpu(), "dk": k.grad.cpu(), "dv": v.grad.cpu(),
+           "dpos_bias": pb.grad.cpu(), "dscale_embed": se.grad.cpu()}
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float32)
+    compare(got, ref, "bf16")
+
+
+def test_fp16_inputs_follow_reference_cast(gpu_device):
+    inp = _rand_inputs(1, 2, 300, 64, OFFSETS_V3, torch.float16, seed=3, gains=False)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    out = dwarf_amd.dsqg_attention_v3(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"])
+    assert out.dtype == torch.float16
+    ref = dsqg_forward(inp["q"].bfloat16().float(), inp["k"].bfloat16().float(),
+                       inp["v"].bfloat16().float(), inp["pos_bias"], inp["scale_embed"])
+    check("out(fp16 via bf16)", out.float().cpu(), ref, "bf16")
+
+
+def test_v3_with_zero_scale_embed_equals_v2(gpu_device):
+    """kernels/dsqg_attention_v3.py:612-628: V3(SE=0) == V2."""
+    inp = _rand_inputs(2, 8, 128, 32, OFFSETS_V3, torch.bfloat16, seed=7, se=False, gains=False)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    o2 = dwarf_amd.dsqg_attention_v2(d["q"], d["k"], d["v"], d["pos_bias"])
+    o3 = dwarf_amd.dsqg_attention_v3(d["q"], d["k"], d["v"], d["pos_bias"],
+                                     torch.zeros(44, 32, device=gpu_device))
+    assert torch.equal(o2, o3)
+
+
+def test_fp32_path_does_not_downcast(gpu_device):
+    inp = _rand_inputs(1, 2, 200, 64, OFFSETS_V3, torch.float32, seed=4, gains=False)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    out = dwarf_amd.dsqg_attention_v3(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"])
+    assert out.dtype == torch.float32
+    ref = dsqg_forward(*(inp[n].double() for n in ("q", "k", "v", "pos_bias", "scale_embed")))
+    check("out fp32", out.cpu(), ref, "fp32")
