@@ -8,6 +8,7 @@ namespace dsqg {
 
 constexpr int kMaxOffsets = 64;   // DSQG_MAX_OFFSETS (size of the offset table in the ABI)
 constexpr int kMaxTaps = 48;      // offsets the kernels hold in registers (J <= 48)
+constexpr int kMaxSparse = 16;    // long-range taps (beyond the dense window) of the MFMA kernels
 constexpr int kMaxWindow = 32;    // largest dense window staged in LDS (delta = 0..32)
 constexpr int kBlock = 256;       // threads per workgroup (4 wave64)
 
@@ -65,6 +66,7 @@ template <> struct Vec8<bf16_t> {
 // Raw 16-byte chunk copy (8 bf16 or 4 f32), used to stage rows into LDS unchanged.
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, uint4 v) { *reinterpret_cast<uint4*>(p) = v; }
+__device__ __forceinline__ uint4 zero16() { return make_uint4(0u, 0u, 0u, 0u); }
 
 // ---------------------------------------------------------------------------------------
 // Cross-lane sums inside aligned groups of G consecutive lanes (G = 1, 2, 4, 8, 16), every

@@ -1,4 +1,5 @@
-// DSQG forward, VALU path (fp32 and bf16).
+// DSQG forward, VALU path: fp32, and bf16 offset tables outside the MFMA kernel's reach
+// (more than kMaxSparse taps beyond the dense window).
 //
 // One workgroup = one (b,h) and a tile of QPB query rows.  Each query row is owned by a group
 // of G = D/8 consecutive lanes, lane g holding elements [8g, 8g+8) of the row, so one row is
@@ -169,7 +170,9 @@ static hipError_t launch_fwd_dtype(const FwdParams& p, int D, hipStream_t st) {
 }
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, hipStream_t st) {
-  return dtype == 0 ? launch_fwd_dtype<float>(p, D, st) : launch_fwd_dtype<bf16_t>(p, D, st);
+  if (dtype == 0) return launch_fwd_dtype<float>(p, D, st);
+  if (fwd_mfma_supported(D, p.taps)) return launch_fwd_mfma(p, D, st);
+  return launch_fwd_dtype<bf16_t>(p, D, st);
 }
 
 }  // namespace dsqg

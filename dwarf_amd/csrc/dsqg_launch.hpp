@@ -9,6 +9,11 @@ namespace dsqg {
 // hipErrorInvalidValue for a head dim without a kernel (the ABI checks that first).
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, hipStream_t st);
 
+// bf16 MFMA forward (dsqg_fwd_mfma.hip): head dims 32/64/128 and at most kMaxSparse taps
+// beyond the dense window.  launch_fwd picks it whenever it applies.
+bool fwd_mfma_supported(int D, const TapTable& t);
+hipError_t launch_fwd_mfma(const FwdParams& p, int D, hipStream_t st);
+
 // Tiling of the backward for these sizes; fills n_tiles / tiles_per_block / n_chunks.
 // With se_grad the dq workgroups cover more rows each, so fewer [J,D] partials are written.
 void bwd_plan(BwdParams& p, int D, bool se_grad);

@@ -1,0 +1,68 @@
+// MFMA and LDS-transpose helpers for the gfx950 bf16 DSQG kernels.
+//
+// Lane layouts (wave64, measured on MI355X):
+//  * v_mfma_f32_16x16x32_bf16: A lane l holds row l%16, k = 8*(l/16) .. +7; B lane l holds
+//    column l%16, k = 8*(l/16) .. +7; C/D lane l holds column l%16, rows 4*(l/16) + r, r=0..3.
+//  * v_mfma_f32_16x16x16_bf16: the same with k = 4*(l/16) .. +3.
+//  * ds_read_tr16_b64: inside each group of 16 lanes, if lane j addresses the 4-element row
+//    M[j][0..3], lane i receives M[4e + i/4][i%4] for e = 0..3.  So with a row-major [row][col]
+//    bf16 tile in LDS, lane i of group g addressing  &T[r0 + 4g + i/4][c0 + 4*(i%4)]  receives
+//    T[r0 + 4g + e][c0 + i], e = 0..3: the transposed 16x16x16 operand (row = column c0+i of
+//    T, k = rows r0+4g .. +3) with no shuffles.
+#pragma once
+
+#include "dsqg_common.hpp"
+
+namespace dsqg {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma_16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4_t mfma_16x16x16(s16x4_t a, s16x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ s16x4_t lds_read_tr16(const bf16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// Four floats -> packed bf16 operand (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ s16x4_t pack_bf16x4(float a, float b, float c, float d) {
+  bf16x4_t r;
+  r[0] = (__bf16)a; r[1] = (__bf16)b; r[2] = (__bf16)c; r[3] = (__bf16)d;
+  return __builtin_bit_cast(s16x4_t, r);
+}
+
+__device__ __forceinline__ uint2 pack_bf16x4_u2(float a, float b, float c, float d) {
+  return __builtin_bit_cast(uint2, pack_bf16x4(a, b, c, d));
+}
+
+__device__ __forceinline__ f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
+
+// Element r (runtime, 0..3) of a 4-vector without dynamic register indexing.
+__device__ __forceinline__ float pick4(f32x4_t v, int r) {
+  const float lo = (r & 1) ? v[1] : v[0];
+  const float hi = (r & 1) ? v[3] : v[2];
+  return (r & 2) ? hi : lo;
+}
+
+// Max / sum over the four lanes {i, i+16, i+32, i+48} that share column i of an MFMA tile.
+__device__ __forceinline__ float col_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+__device__ __forceinline__ float col_sum(float x) {
+  x += __shfl_xor(x, 16, 64);
+  return x + __shfl_xor(x, 32, 64);
+}
+
+}  // namespace dsqg

@@ -171,6 +171,27 @@ def test_other_offset_tables(gpu_device, offsets, N):
     compare(got, ref, "fp32")
 
 
+@pytest.mark.parametrize("offsets,N", [(OFFSETS_J47, 4097), ((0, 1, 2, 5, 9, 100), 300), ((0,), 40),
+                                       (tuple(range(0, 96, 2)), 200)])
+def test_other_offset_tables_bf16(gpu_device, offsets, N):
+    """bf16 over other tables; the last one (47 taps beyond a 1-row window) exceeds the MFMA
+    kernel's 16 long-range taps and runs the VALU kernel."""
+    inp = _rand_inputs(1, 3, N, 64, offsets, torch.bfloat16, seed=len(offsets) + 1)
+    _say(f"bf16 offsets J={len(offsets)} N={N}")
+    got = gpu_run(inp, offsets, gpu_device)
+    ref = oracle_chunked(inp, offsets, torch.float32)
+    compare(got, ref, "bf16")
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+def test_bf16_head_dims_all_parameters(gpu_device, D):
+    inp = _rand_inputs(2, 3, 1700, D, OFFSETS_V3, torch.bfloat16, seed=200 + D)
+    _say(f"bf16 fwd+bwd B2 H3 N1700 D{D} with se, g, a")
+    got = gpu_run(inp, OFFSETS_V3, gpu_device)
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float32)
+    compare(got, ref, "bf16")
+
+
 def test_empty_inputs(gpu_device):
     for shape in ((0, 2, 16, 64), (1, 2, 0, 64)):
         inp = _rand_inputs(*shape, OFFSETS_V3, torch.bfloat16, seed=1)
