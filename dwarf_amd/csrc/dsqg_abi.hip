@@ -89,9 +89,11 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   if (ne > 0 && !a->lse) return DSQG_EINVAL;
   if ((long long)s.J * s.H > 0 && (!a->pos_bias || !a->dpos_bias)) return DSQG_EINVAL;
   p->B = s.B; p->H = s.H; p->N = s.N;
-  bwd_plan(*p, s.D, a->dscale_embed != nullptr);
+  p->qs = to_strides(a->q_stride); p->ks = to_strides(a->k_stride);
+  p->vs = to_strides(a->v_stride); p->dos = to_strides(a->dout_stride);
+  bwd_plan(*p, s.D, s.dtype, a->dscale_embed != nullptr);
   if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;
-  if ((long long)s.B * s.H * p->n_tiles > INT_MAX / 2) return DSQG_EINVAL;
+  if ((long long)s.B * s.H * p->n_tiles_kv > INT_MAX / 2) return DSQG_EINVAL;
   return DSQG_OK;
 }
 
@@ -193,7 +195,7 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
     if ((st = hip_status(launch_bwd_dq(p, s.dtype, s.D, nb, hs)))) return st;
   }
   if ((phases & kPhaseDkdv) && rows) {
-    const unsigned nb = (unsigned)((long long)s.B * s.H * p.n_tiles);
+    const unsigned nb = (unsigned)((long long)s.B * s.H * p.n_tiles_kv);
     if ((st = hip_status(launch_bwd_dkdv(p, s.dtype, s.D, nb, hs)))) return st;
   }
   if (phases & kPhaseParams) {

@@ -57,9 +57,21 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
   }
 }
 
-void bwd_plan(BwdParams& p, int D, bool se_grad) {
-  const int QPB = kBlock / (D / 8);
+bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
+  if (dtype != 1) return false;
+  long long rs = p.qs.n, rmin = p.qs.n;
+  const long long all[4] = {p.qs.n, p.ks.n, p.vs.n, p.dos.n};
+  for (long long x : all) { rs = x > rs ? x : rs; rmin = x < rmin ? x : rmin; }
+  const long long span = ((long long)p.N + p.taps.maxd + 64) * rs * 2;
+  return (D == 32 || D == 64 || D == 128) && p.taps.J - p.taps.W - 1 <= kMaxSparse &&
+         rmin >= D && span < (1LL << 31);
+}
+
+void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
+  const int QPB = bwd_mfma_supported(p, D, dtype) ? 64 : kBlock / (D / 8);
+  const int KPB = kBlock / (D / 8);  // dk/dv kernel rows per workgroup
   p.n_tiles = (p.N + QPB - 1) / QPB;
+  p.n_tiles_kv = (p.N + KPB - 1) / KPB;
   const long long work = (long long)p.B * p.H * p.n_tiles;
   const long long target = se_grad ? 1024 : 4096;
   int tpb = (int)((work + target - 1) / target);

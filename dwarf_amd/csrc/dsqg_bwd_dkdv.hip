@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dkdv_kernel(BwdParams p) {
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
-  const int bh = lb / p.n_tiles, tile = lb - bh * p.n_tiles;
+  const int bh = lb / p.n_tiles_kv, tile = lb - bh * p.n_tiles_kv;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;
   const float c = p.scale;

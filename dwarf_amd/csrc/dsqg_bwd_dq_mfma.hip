@@ -1,0 +1,437 @@
+// DSQG backward, launch 1, bf16 MFMA path (gfx950): query-centric dq, D' and the per-workgroup
+// parameter-gradient partials.
+//
+// A workgroup owns one (b,h) and a run of 64-row query tiles; wave w owns rows n0+16w .. +15 of
+// the tile.  With lse from the forward, every weight alpha_j = exp(s_j - lse) is known as soon
+// as its score is, so the taps stream through once:
+//   u_j   = dOut . v_j                      (U^T = V dOut^T on the MFMA, like S^T = K Q^T)
+//   D'   += alpha_j u_j
+//   X    += g_j alpha_j (u_j - D0) k_j,   Y += g_j alpha_j k_j   (K^T from LDS, ds_read_tr16_b64)
+// and at the end dq = c (a (X - (D' - D0) Y) + sum_j dS_j se_j) with dS_j = a alpha_j (u_j - D').
+// This is sum_j dS_j (c g_j k_j + c se_j), the gradient of s_j = c g_j q.k_j + b_j + c q.se_j.
+// D0, the dense band's alpha-weighted mean of u, is known before the first product; taking it
+// out of u before the bf16 rounding of the operands keeps their error proportional to u - D'.
+// The dense band and the long-range taps are laid out as in the forward (dsqg_fwd_mfma.hip):
+// band keys [n0w-32, n0w+16) as three 16x16 tiles, long-range taps as the diagonal of one tile.
+// dS is then written to a per-wave [query][tap] table in LDS, from which the workgroup sums
+// dbias (and dg, da) in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS).
+//
+// Follows _compute_D_v3 + _bwd_dq_v3 (kernels/dsqg_attention_v3.py:170-275), except that D' is
+// computed from the fp32 weights and the parameter gradients avoid atomics.
+#include "dsqg_common.hpp"
+#include "dsqg_launch.hpp"
+#include "dsqg_mfma.hpp"
+
+namespace dsqg {
+
+template <int D, bool HAS_SE, int NSC>
+__global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
+  constexpr int QT = 64;
+  constexpr int KS = D / 32;
+  constexpr int DB = D / 16;
+  constexpr int RV = D + 16;              // LDS row stride for transposing reads
+  constexpr int WIN = QT + kMaxWindow;
+  constexpr int CPR = D / 8;
+  constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
+  constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
+  constexpr int PF = 2;                   // long-range K/V operands loaded ahead of use
+  constexpr int TS = 52;                  // row stride of the per-wave [query][tap] tables (16 B aligned)
+  constexpr int SEJ = 48;                 // scale_embed rows staged (J <= 48)
+  constexpr int SE_PER_T = (SEJ * D + kBlock - 1) / kBlock;
+  constexpr float kLog2e = 1.4426950408889634f;
+
+  __shared__ __align__(16) bf16_t sK[WIN * RV];        // dense-window K rows (transposing reads)
+  __shared__ __align__(16) bf16_t sKs[4][16 * RV];     // wave-private long-range K block
+  __shared__ __align__(16) bf16_t sQ[HAS_SE ? 4 * 16 * RV : 8];   // wave's Q rows (for dse)
+  __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];     // scale_embed rows, bf16
+  __shared__ float sT[HAS_SE ? 4 * 16 * TS : 1];       // log2e * (bias + c q.se)
+  __shared__ __align__(16) float sDS[4 * 16 * TS];      // dS[query][tap] per wave
+  __shared__ float sRAW[4 * 16 * TS];                   // c q.k per (query, tap), for dg
+  __shared__ float sBias2[kMaxTaps];
+  __shared__ float sGain2[kMaxTaps];                    // gain * c * log2e
+  __shared__ float sGain[kMaxTaps];
+  __shared__ float sDp[4 * 16];
+
+  const int tid = threadIdx.x;
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int bh = lb / p.n_chunks, chunk = lb - bh * p.n_chunks;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int N = p.N, J = p.taps.J, W = p.taps.W;
+  const int NS = NSC > 0 ? NSC : J - W - 1;
+  const float c = p.scale, c2 = p.scale * kLog2e;
+  const float a = p.if_gain ? p.if_gain[h] : 1.0f;
+  const bool se_grad = p.part_se != nullptr, g_grad = p.part_gain != nullptr;
+  const int qsn = (int)p.qs.n, ksn = (int)p.ks.n, vsn = (int)p.vs.n, dosn = (int)p.dos.n;
+
+  const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rK = slice_rsrc(static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h, p.ks.n, N, D);
+  const __amdgpu_buffer_rsrc_t rV = slice_rsrc(static_cast<const bf16_t*>(p.v) + b * p.vs.b + h * p.vs.h, p.vs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rO = slice_rsrc(static_cast<const bf16_t*>(p.dout) + b * p.dos.b + h * p.dos.h, p.dos.n, N, D);
+  bf16_t* dqb = static_cast<bf16_t*>(p.dq) + b * p.dqs.b + h * p.dqs.h;
+  const long long rowbase = ((long long)b * p.H + h) * N;
+
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 15, g = l >> 4;
+  const int qlane = opaque(i * qsn + 8 * g), klane = opaque(i * ksn + 8 * g);
+  const int vlane = opaque(i * vsn + 8 * g), olane = opaque(i * dosn + 8 * g);
+
+  for (int j = tid; j < J; j += kBlock) {
+    const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
+    sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
+    sGain2[j] = gj * c2;
+    sGain[j] = gj;
+  }
+  if constexpr (HAS_SE) {
+    for (int e = tid; e < SEJ * D; e += kBlock) {
+      const int j = e / D, d = e - j * D;
+      const __bf16 x = (__bf16)(j < J && p.scale_embed ? p.scale_embed[j * D + d] : 0.f);
+      sSE[j * RV + d] = __builtin_bit_cast(bf16_t, x);
+    }
+  }
+
+  // Table columns J..47 are read as zeros (whole 4-wide groups feed the MFMA operands).
+  for (int e = tid; e < 4 * 16 * (48 - J); e += kBlock) {
+    const int row = e / (48 - J), j = J + e % (48 - J);
+    sDS[row * TS + j] = 0.f;
+    sRAW[row * TS + j] = 0.f;
+  }
+
+  float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
+  f32x4_t accSE[HAS_SE ? 3 : 1][HAS_SE ? DB : 1];
+#pragma unroll
+  for (int jb = 0; jb < (HAS_SE ? 3 : 1); ++jb)
+#pragma unroll
+    for (int db = 0; db < (HAS_SE ? DB : 1); ++db) accSE[jb][db] = zero4();
+
+  float* sDSw = sDS + w * 16 * TS;
+  float* sRAWw = sRAW + w * 16 * TS;
+  float* sTw = sT + (HAS_SE ? w * 16 * TS : 0);
+  bf16_t* sKsw = sKs[w];
+  const int t_begin = chunk * p.tiles_per_block;
+  const int t_end = min(p.n_tiles, t_begin + p.tiles_per_block);
+
+  for (int tile = t_begin; tile < t_end; ++tile) {
+    const int n0 = tile * QT;
+    const int n0w = n0 + 16 * w;
+    const int n = n0w + i;
+    const bool row_ok = n < N;
+
+    // ---- Loads (zero outside [0, N)). ----
+    uint4 wk[CWIN];
+#pragma unroll
+    for (int u = 0; u < CWIN; ++u) {
+      const int ci = tid + u * kBlock;
+      wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque((ci / CPR) * ksn + (ci % CPR) * 8));
+    }
+    bf16x8_t qB[KS], oB[KS];
+    uint4 kD[3][KS], vD[3][KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
+      oB[s] = as_bf16x8(bload16(rO, n0w * dosn + olane + 32 * s));
+    }
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        kD[kk][s] = bload16(rK, (n0w - 32 + 16 * kk) * ksn + klane + 32 * s);
+        vD[kk][s] = bload16(rV, (n0w - 32 + 16 * kk) * vsn + vlane + 32 * s);
+      }
+    const float lse2 = row_ok ? p.lse[rowbase + n] * kLog2e : 0.f;
+    uint4 kS[PF][KS], vS[PF][KS];
+#pragma unroll
+    for (int t = 0; t < PF; ++t) {
+      if (t < NS) {
+        const int m0 = n0w - p.taps.delta[W + 1 + t];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          kS[t][s] = bload16(rK, m0 * ksn + klane + 32 * s);
+          vS[t][s] = bload16(rV, m0 * vsn + vlane + 32 * s);
+        }
+      }
+    }
+
+    __syncthreads();  // previous tile's readers of sK / tables are done
+#pragma unroll
+    for (int u = 0; u < CWIN; ++u) {
+      const int ci = tid + u * kBlock;
+      if (ci < WIN * CPR) st16(sK + (ci / CPR) * RV + (ci % CPR) * 8, wk[u]);
+    }
+    if constexpr (HAS_SE) {
+      // The wave's Q rows (B layout: row i, chunks 8g + 32s) as natural rows, for dse.
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        *reinterpret_cast<bf16x8_t*>(sQ + (w * 16 + i) * RV + 8 * g + 32 * s) = qB[s];
+    }
+    __syncthreads();
+
+    // ---- Dense band: S^T = K Q^T, U^T = V dOut^T. ----
+    f32x4_t accS[3], accU[3];
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      accS[kk] = zero4();
+      accU[kk] = zero4();
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        accS[kk] = mfma_16x16x32(as_bf16x8(kD[kk][s]), qB[s], accS[kk]);
+        accU[kk] = mfma_16x16x32(as_bf16x8(vD[kk][s]), oB[s], accU[kk]);
+      }
+    }
+    if constexpr (HAS_SE) {
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        f32x4_t acc = zero4();
+        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * jb + 4 * g + r;
+          if (j < J) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+    }
+
+    // Dense weights first; D0 = the band's weighted mean of u is subtracted from u before the
+    // bf16 rounding of the dQ operands, so their error scales with u - D' rather than u.
+    float al[12], uu[12];
+    float dlane = 0.f, wlane = 0.f;
+    const int dl0 = 32 - 4 * g + i;
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int dl = dl0 - 16 * kk - r;
+        const bool ok = row_ok && (unsigned)dl <= (unsigned)W && n >= dl;
+        const int j = ok ? dl : 0;
+        const float s2 = fmaf(sGain2[j], accS[kk][r], HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+        const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
+        al[4 * kk + r] = alpha;
+        uu[4 * kk + r] = accU[kk][r];
+        dlane = fmaf(alpha, accU[kk][r], dlane);
+        wlane += alpha;
+      }
+    }
+    const float wsum = col_sum(wlane);
+    const float D0 = wsum > 0.f ? col_sum(dlane) / wsum : 0.f;
+    f32x4_t X[DB], Y[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db) { X[db] = zero4(); Y[db] = zero4(); }
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk) {
+      float ga[4], gau[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int dl = dl0 - 16 * kk - r;
+        const int j = (unsigned)dl <= (unsigned)W ? dl : 0;
+        ga[r] = sGain[j] * al[4 * kk + r];
+        gau[r] = ga[r] * (uu[4 * kk + r] - D0);
+      }
+      const s16x4_t b1 = pack_bf16x4(gau[0], gau[1], gau[2], gau[3]);
+      const s16x4_t b2 = pack_bf16x4(ga[0], ga[1], ga[2], ga[3]);
+      const bf16_t* kr = sK + (16 * w + 16 * kk + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const s16x4_t at = lds_read_tr16(kr + 16 * db);
+        X[db] = mfma_16x16x16(at, b1, X[db]);
+        Y[db] = mfma_16x16x16(at, b2, Y[db]);
+      }
+    }
+
+    // ---- Long-range taps (diagonal of one 16x16 tile each). ----
+    const bool diag = g == (i >> 2);
+    float als[NSM], uus[NSM], raws[NSM];
+    const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+    for (int t = 0; t < NSM; ++t) {
+      als[t] = 0.f; uus[t] = 0.f; raws[t] = 0.f;
+      if (NSC > 0 || t < NS) {
+        const int j = W + 1 + t;
+        f32x4_t as = zero4(), au = zero4();
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          as = mfma_16x16x32(as_bf16x8(kS[t % PF][s]), qB[s], as);
+          au = mfma_16x16x32(as_bf16x8(vS[t % PF][s]), oB[s], au);
+        }
+        // Stage the key rows (A layout: row i, chunks 8g + 32s) for the transposing reads.
+#pragma unroll
+        for (int s = 0; s < KS; ++s) st16(sKsw + i * RV + 8 * g + 32 * s, kS[t % PF][s]);
+        if (t + PF < NS) {
+          const int m0 = n0w - p.taps.delta[W + 1 + t + PF];
+#pragma unroll
+          for (int s = 0; s < KS; ++s) {
+            kS[t % PF][s] = bload16(rK, m0 * ksn + klane + 32 * s);
+            vS[t % PF][s] = bload16(rV, m0 * vsn + vlane + 32 * s);
+          }
+        }
+        const float raw = pick4(as, i & 3), uval = pick4(au, i & 3);
+        const bool ok = diag && row_ok && n >= p.taps.delta[j];
+        const float s2 = fmaf(sGain2[j], raw, HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+        const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
+        als[t] = alpha;
+        uus[t] = uval;
+        raws[t] = raw;
+        dlane = fmaf(alpha, uval, dlane);
+        const float gal = sGain[j] * alpha;
+        const s16x4_t b1 = onehot_bf16x4(gal * (uval - D0), i & 3);
+        const s16x4_t b2 = onehot_bf16x4(gal, i & 3);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const s16x4_t at = lds_read_tr16(ksr + 16 * db);
+          X[db] = mfma_16x16x16(at, b1, X[db]);
+          Y[db] = mfma_16x16x16(at, b2, Y[db]);
+        }
+      }
+    }
+
+    const float Dp = col_sum(dlane);  // D' = dOut . o (pre-gain o) for query n
+
+    // ---- dS table [query][tap] (every entry j < J is written: zero where masked). ----
+#pragma unroll
+    for (int kk = 0; kk < 3; ++kk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int dl = dl0 - 16 * kk - r;
+        if ((unsigned)dl <= (unsigned)W) {
+          const float dS = a * al[4 * kk + r] * (uu[4 * kk + r] - Dp);
+          sDSw[i * TS + dl] = dS;
+          sRAWw[i * TS + dl] = c * accS[kk][r];
+        }
+      }
+    if (diag) {
+#pragma unroll
+      for (int t = 0; t < NSM; ++t)
+        if (NSC > 0 || t < NS) {
+          sDSw[i * TS + W + 1 + t] = a * als[t] * (uus[t] - Dp);
+          sRAWw[i * TS + W + 1 + t] = c * raws[t];
+        }
+    }
+    if (g == 0) sDp[w * 16 + i] = row_ok ? Dp : 0.f;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+
+    // dq = c (a (X - D' Y) + SE^T dS^T)
+    f32x4_t dQ[DB];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dQ[db][r] = a * (X[db][r] - (Dp - D0) * Y[db][r]);
+    if constexpr (HAS_SE) {
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
+        const s16x4_t bs = pack_bf16x4(d4.x, d4.y, d4.z, d4.w);
+        const bf16_t* sr = sSE + (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) dQ[db] = mfma_16x16x16(lds_read_tr16(sr + 16 * db), bs, dQ[db]);
+      }
+    }
+    if (row_ok) {
+      bf16_t* o = dqb + n * p.dqs.n + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        *reinterpret_cast<uint2*>(o + 16 * db) =
+            pack_bf16x4_u2(c * dQ[db][0], c * dQ[db][1], c * dQ[db][2], c * dQ[db][3]);
+      if (g == 0) p.dpre[rowbase + n] = Dp;
+    }
+
+    // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j), per wave.
+    if constexpr (HAS_SE) {
+      if (se_grad) {
+        const bf16_t* qr = sQ + (w * 16 + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+        for (int jb = 0; jb < 3; ++jb) {
+          const float* col = sDSw + (4 * g) * TS + 16 * jb + i;
+          const s16x4_t bs = pack_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS]);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            accSE[jb][db] = mfma_16x16x16(lds_read_tr16(qr + 16 * db), bs, accSE[jb][db]);
+        }
+      }
+    }
+    __syncthreads();  // all waves' tables are complete
+    if (tid < J) {
+      float sb = 0.f, sg = 0.f;
+      for (int q = 0; q < 64; ++q) {
+        const float ds = sDS[q * TS + tid];  // wave q/16, query q%16: [w][i] rows are contiguous
+        sb += ds;
+        sg = fmaf(ds, sRAW[q * TS + tid], sg);
+      }
+      acc_bias += sb;
+      acc_gain += sg;
+    }
+    if (tid == 0) {
+      float sa = 0.f;
+      for (int q = 0; q < 64; ++q) sa += sDp[q];
+      acc_if += sa;
+    }
+  }
+
+  if (tid < J) {
+    p.part_bias[(long long)lb * J + tid] = acc_bias;
+    if (g_grad) p.part_gain[(long long)lb * J + tid] = acc_gain;
+  }
+  if (tid == 0 && p.part_if) p.part_if[lb] = acc_if;
+  if constexpr (HAS_SE) {
+    if (se_grad) {
+      // Reduce the four waves' [d][j] accumulators through LDS (reusing the dS tables), fixed order.
+      __syncthreads();
+      float* red = sDS;  // 4 * 16 * TS floats >= 4 waves * 3 * DB * 64 lanes * 4 values / ...
+      for (int jb = 0; jb < 3; ++jb) {
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          // lane (i, g) holds dSE^T[d = 16db + 4g + r][j = 16jb + i]
+#pragma unroll
+          for (int r = 0; r < 4; ++r) red[(w * 64 + l) * 4 + r] = accSE[jb][db][r];
+          __syncthreads();
+          if (tid < 64) {
+            const int ii = tid & 15, gg = tid >> 4;
+            const int j = 16 * jb + ii;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float sum = 0.f;
+#pragma unroll
+              for (int ww = 0; ww < 4; ++ww) sum += red[(ww * 64 + tid) * 4 + r];
+              const int d = 16 * db + 4 * gg + r;
+              if (j < J) p.part_se[((long long)lb * J + j) * D + d] = c * sum;
+            }
+          }
+          __syncthreads();
+        }
+      }
+    }
+  }
+}
+
+template <int D, bool HAS_SE>
+static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
+  switch (p.taps.J - p.taps.W - 1) {
+    case 11: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 11>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 13: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 13>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 14: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 14>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    default: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0>), dim3(nb), dim3(kBlock), 0, st, p); break;
+  }
+}
+
+template <int D>
+static hipError_t launch_dq_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
+  // The scale_embed variant also serves dse requested at se = 0.
+  if (p.scale_embed || p.part_se) launch_dq_mfma_ns<D, true>(p, nb, st);
+  else launch_dq_mfma_ns<D, false>(p, nb, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dq_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st) {
+  switch (D) {
+    case 32: return launch_dq_mfma_d<32>(p, nblocks, st);
+    case 64: return launch_dq_mfma_d<64>(p, nblocks, st);
+    case 128: return launch_dq_mfma_d<128>(p, nblocks, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace dsqg

@@ -134,9 +134,10 @@ struct FwdParams {
 
 struct BwdParams {
   int B, H, N;
-  int n_tiles;      // row tiles per (b,h)
+  int n_tiles;          // query tiles per (b,h) of the dq launch
   int tiles_per_block;  // consecutive tiles of one (b,h) handled by one dq workgroup
-  int n_chunks;     // dq workgroups per (b,h)
+  int n_chunks;         // dq workgroups per (b,h)
+  int n_tiles_kv;       // key tiles per (b,h) of the dk/dv launch (one workgroup each)
   float scale;
   TapTable taps;
   const void* q; Strides4 qs;

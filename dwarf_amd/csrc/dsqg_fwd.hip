@@ -171,7 +171,7 @@ static hipError_t launch_fwd_dtype(const FwdParams& p, int D, hipStream_t st) {
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, hipStream_t st) {
   if (dtype == 0) return launch_fwd_dtype<float>(p, D, st);
-  if (fwd_mfma_supported(D, p.taps)) return launch_fwd_mfma(p, D, st);
+  if (fwd_mfma_supported(p, D)) return launch_fwd_mfma(p, D, st);
   return launch_fwd_dtype<bf16_t>(p, D, st);
 }
 

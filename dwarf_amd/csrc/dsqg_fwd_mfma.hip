@@ -27,196 +27,229 @@
 
 namespace dsqg {
 
-// Loads this thread's 16-byte chunks of the 64-row block starting at row r0 (zero outside
-// [0, N)) into registers; chunk c of the block is row c / CPR, column chunk c % CPR.
-template <int CH, int CPR>
-__device__ __forceinline__ void stage_rows(uint4 (&stg)[CH], const bf16_t* base, long long rs,
-                                           int r0, int N, int tid) {
-#pragma unroll
-  for (int cI = 0; cI < CH; ++cI) {
-    const int chunk = tid + cI * kBlock;
-    const int r = chunk / CPR, cc = chunk - r * CPR;
-    const int m = r0 + r;
-    stg[cI] = (m >= 0 && m < N) ? ld16(base + m * rs + cc * 8) : zero16();
-  }
-}
+template <int D, bool HAS_SE, int NSC>
+__global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
+  constexpr int QT = 64;                  // query rows per workgroup
+  constexpr int KS = D / 32;              // 16x16x32 steps over the head dim
+  constexpr int DB = D / 16;              // 16-wide head-dim blocks of the output
+  constexpr int RV = D + 16;              // LDS row stride of V tiles (transposing reads)
+  constexpr int WIN = QT + kMaxWindow;    // dense-window rows of V staged in LDS
+  constexpr int CPR = D / 8;              // 16-byte chunks per row
+  constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
+  constexpr int CHW = 16 * CPR / 64;      // chunks per lane of a wave's 16-row block
+  static_assert(16 * CPR % 64 == 0, "a wave's 16-row block must split evenly over 64 lanes");
+  constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
+  constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
+  constexpr int TS = 49;                  // row stride of the per-wave T table
+  constexpr float kLog2e = 1.4426950408889634f;
 
-template <int D, bool HAS_SE>
-__global__ __launch_bounds__(kBlock) void fwd_mfma_kernel(FwdParams p) {
-  constexpr int QT = 64;                 // query rows per workgroup
-  constexpr int KS = D / 32;             // 16x16x32 steps over the head dim
-  constexpr int DB = D / 16;             // 16-wide head-dim blocks of the output
-  constexpr int RK = D + 8;              // LDS row stride of K (16-byte natural reads)
-  constexpr int RV = D + 16;             // LDS row stride of V (transposing reads)
-  constexpr int WIN = QT + kMaxWindow;   // staged dense-window rows
-  constexpr int CPR = D / 8;             // 16-byte chunks per row
-  constexpr int CH = QT * CPR / kBlock;  // chunks per thread when staging a 64-row block
-  constexpr int TS = 49;                 // row stride of the per-wave T table
-
-  __shared__ __align__(16) bf16_t sK[WIN * RK];
   __shared__ __align__(16) bf16_t sV[WIN * RV];
-  __shared__ __align__(16) bf16_t sVs[2][QT * RV];
-  __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * RK : 8];
+  __shared__ __align__(16) bf16_t sVs[4][16 * RV];   // wave-private long-range V block
+  __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
   __shared__ float sT[HAS_SE ? 4 * 16 * TS : 1];
-  __shared__ float sBias[kMaxTaps];
-  __shared__ float sGain[kMaxTaps];
+  __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
+  __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
   const int bh = lb / p.n_tiles, tile = lb - bh * p.n_tiles;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;
-  const int NS = J - W - 1;
+  const int NS = NSC > 0 ? NSC : J - W - 1;
   const int n0 = tile * QT;
-  const float c = p.scale;
+  const float c2 = p.scale * kLog2e;
+  const int qsn = (int)p.qs.n, ksn = (int)p.ks.n, vsn = (int)p.vs.n;
 
-  const bf16_t* qb = static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h;
-  const bf16_t* kb = static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h;
-  const bf16_t* vb = static_cast<const bf16_t*>(p.v) + b * p.vs.b + h * p.vs.h;
+  const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rK = slice_rsrc(static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h, p.ks.n, N, D);
+  const __amdgpu_buffer_rsrc_t rV = slice_rsrc(static_cast<const bf16_t*>(p.v) + b * p.vs.b + h * p.vs.h, p.vs.n, N, D);
 
-  for (int ci = tid; ci < WIN * CPR; ci += kBlock) {
-    const int r = ci / CPR, cc = ci - r * CPR;
-    const int m = n0 - kMaxWindow + r;
-    const bool ok = m >= 0 && m < N;
-    st16(sK + r * RK + cc * 8, ok ? ld16(kb + m * p.ks.n + cc * 8) : zero16());
-    st16(sV + r * RV + cc * 8, ok ? ld16(vb + m * p.vs.n + cc * 8) : zero16());
+  // The wave index is uniform: readfirstlane keeps every row product on the scalar unit.
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 15, g = l >> 4;
+  const int n0w = n0 + 16 * w;
+  const int n = n0w + i;  // query row of this lane's MFMA column
+  const bool row_ok = n < N;
+
+  // ---- Global loads (all zero-filled outside [0, N) by the buffer range check). ----
+  // Offsets are (uniform row) * stride + (per-lane part), so the row products stay scalar.
+  uint4 wv[CWIN];
+#pragma unroll
+  for (int u = 0; u < CWIN; ++u) {
+    const int ci = tid + u * kBlock;
+    wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque((ci / CPR) * vsn + (ci % CPR) * 8));
+  }
+  const int qlane = opaque(i * qsn + 8 * g), klane = opaque(i * ksn + 8 * g);
+  bf16x8_t qB[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
+  uint4 kD[3][KS];   // dense band: key rows n0w-32+16kk+i as A operands
+#pragma unroll
+  for (int kk = 0; kk < 3; ++kk)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kD[kk][s] = bload16(rK, (n0w - 32 + 16 * kk) * ksn + klane + 32 * s);
+  // Long-range key rows n0w - delta + i, loaded in two halves (the second after the dense band
+  // has consumed its registers) to bound the register peak.
+  constexpr int NH = (NSM + 1) / 2;
+  uint4 kS[NSM][KS];
+#pragma unroll
+  for (int t = 0; t < NH; ++t) {
+    if (NSC > 0 || t < NS) {
+      const int m0 = n0w - p.taps.delta[W + 1 + t];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kS[t][s] = bload16(rK, m0 * ksn + klane + 32 * s);
+    }
   }
   for (int j = tid; j < J; j += kBlock) {
-    sBias[j] = p.pos_bias[j * p.H + h];
-    sGain[j] = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
+    sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
+    sGain2[j] = (p.score_gain ? p.score_gain[h * J + j] : 1.0f) * c2;
   }
   if constexpr (HAS_SE) {
     for (int e = tid; e < 48 * D; e += kBlock) {
       const int j = e / D, d = e - j * D;
       const __bf16 x = (__bf16)(j < J ? p.scale_embed[j * D + d] : 0.f);
-      sSE[j * RK + d] = __builtin_bit_cast(bf16_t, x);
+      sSE[j * (D + 8) + d] = __builtin_bit_cast(bf16_t, x);
     }
+  }
+#pragma unroll
+  for (int u = 0; u < CWIN; ++u) {
+    const int ci = tid + u * kBlock;
+    const int r = ci / CPR, cc = ci - r * CPR;
+    if (ci < WIN * CPR) st16(sV + r * RV + cc * 8, wv[u]);
   }
   __syncthreads();
 
-  const int w = tid >> 6, l = tid & 63, i = l & 15, g = l >> 4;
-  const int n0w = n0 + 16 * w;
-  const int n = n0w + i;  // query row of this lane's MFMA column
-  const bool row_ok = n < N;
-
-  bf16x8_t qB[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s)
-    qB[s] = as_bf16x8(row_ok ? ld16(qb + n * p.qs.n + 32 * s + 8 * g) : zero16());
-
-  // Dense band scores.
+  // ---- Dense band scores: S^T = K_band Q^T. ----
   f32x4_t accS[3];
 #pragma unroll
   for (int kk = 0; kk < 3; ++kk) {
     accS[kk] = zero4();
-    const bf16_t* kr = sK + (16 * w + 16 * kk + i) * RK + 8 * g;
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
+    for (int s = 0; s < KS; ++s) accS[kk] = mfma_16x16x32(as_bf16x8(kD[kk][s]), qB[s], accS[kk]);
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = NH; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
+      const int m0 = n0w - p.taps.delta[W + 1 + t];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kS[t][s] = bload16(rK, m0 * ksn + klane + 32 * s);
+    }
+  }
+  int vlane[CHW];  // this lane's chunks of a wave's 16-row V block
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) vlane[u] = opaque(((l + 64 * u) / CPR) * vsn + ((l + 64 * u) % CPR) * 8);
+  uint4 vS[PF][CHW];  // long-range V rows n0w - delta + 0..15, PF taps ahead
+#pragma unroll
+  for (int t = 0; t < PF; ++t) {
+    if (t < NS) {
+      const int r0 = n0w - p.taps.delta[W + 1 + t];
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) vS[t][u] = bload16(rV, r0 * vsn + vlane[u]);
+    }
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
 
   float* sTw = sT + (HAS_SE ? w * 16 * TS : 0);
   if constexpr (HAS_SE) {
 #pragma unroll
     for (int jb = 0; jb < 3; ++jb) {
       f32x4_t acc = zero4();
-      const bf16_t* sr = sSE + (16 * jb + i) * RK + 8 * g;
+      const bf16_t* sr = sSE + (16 * jb + i) * (D + 8) + 8 * g;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
         acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * jb + 4 * g + r;
-        if (j < J) sTw[i * TS + j] = fmaf(c, acc[r], sBias[j]);
+        if (j < J) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's table is written
+    __builtin_amdgcn_wave_barrier();
   }
 
+  // Scores in log2 units: s2 = gain*c*log2e * q.k + log2e*(bias + c q.se).
   float sd[12];
+  const int dl0 = 32 - 4 * g + i;
 #pragma unroll
   for (int kk = 0; kk < 3; ++kk) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int dl = 32 - 16 * kk - 4 * g - r + i;  // n - m for key m of this register
-      const bool ok = row_ok && dl >= 0 && dl <= W && n - dl >= 0;
+      const int dl = dl0 - 16 * kk - r;  // n - m for key m of this register
+      const bool ok = row_ok && (unsigned)dl <= (unsigned)W && n >= dl;
       const int j = ok ? dl : 0;
-      sd[kk * 4 + r] = ok ? fmaf(c * sGain[j], accS[kk][r], HAS_SE ? sTw[i * TS + j] : sBias[j]) : -INFINITY;
+      const float v = fmaf(sGain2[j], accS[kk][r], HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+      sd[kk * 4 + r] = ok ? v : -INFINITY;
     }
   }
 
   const bool diag = g == (i >> 2);
-  float ss[kMaxSparse];
+  float ss[NSM];
 #pragma unroll
-  for (int t = 0; t < kMaxSparse; ++t) {
+  for (int t = 0; t < NSM; ++t) {
     ss[t] = -INFINITY;
-    if (t < NS) {
+    if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      const int dl = p.taps.delta[j];
-      const int mrow = n0w + i - dl;  // key row feeding A row i
-      const bool in = mrow >= 0 && mrow < N;
       f32x4_t acc = zero4();
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = mfma_16x16x32(as_bf16x8(in ? ld16(kb + mrow * p.ks.n + 32 * s + 8 * g) : zero16()), qB[s], acc);
-      const float raw = pick4(acc, i & 3);
-      if (diag && row_ok && n - dl >= 0) ss[t] = fmaf(c * sGain[j], raw, HAS_SE ? sTw[i * TS + j] : sBias[j]);
+      for (int s = 0; s < KS; ++s) acc = mfma_16x16x32(as_bf16x8(kS[t][s]), qB[s], acc);
+      const float v = fmaf(sGain2[j], pick4(acc, i & 3), HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+      ss[t] = (diag && row_ok && n >= p.taps.delta[j]) ? v : -INFINITY;
     }
   }
 
+  // ---- Softmax over the J taps of each query column (base 2). ----
   float mx = -INFINITY;
 #pragma unroll
   for (int e = 0; e < 12; ++e) mx = fmaxf(mx, sd[e]);
 #pragma unroll
-  for (int t = 0; t < kMaxSparse; ++t) mx = fmaxf(mx, ss[t]);
+  for (int t = 0; t < NSM; ++t) mx = fmaxf(mx, ss[t]);
   mx = col_max(mx);
   if (mx == -INFINITY) mx = 0.f;  // row past N
   float lsum = 0.f;
 #pragma unroll
-  for (int e = 0; e < 12; ++e) { sd[e] = __expf(sd[e] - mx); lsum += sd[e]; }
+  for (int e = 0; e < 12; ++e) { sd[e] = __builtin_amdgcn_exp2f(sd[e] - mx); lsum += sd[e]; }
 #pragma unroll
-  for (int t = 0; t < kMaxSparse; ++t) { ss[t] = __expf(ss[t] - mx); lsum += ss[t]; }
+  for (int t = 0; t < NSM; ++t) { ss[t] = __builtin_amdgcn_exp2f(ss[t] - mx); lsum += ss[t]; }
   lsum = col_sum(lsum);
   const long long rowbase = ((long long)b * p.H + h) * N;
-  if (row_ok && g == 0 && p.lse) p.lse[rowbase + n] = mx + __logf(lsum);
+  if (row_ok && g == 0 && p.lse) p.lse[rowbase + n] = (mx + __log2f(lsum)) * 0.6931471805599453f;
   const float a = p.if_gain ? p.if_gain[h] : 1.0f;
   const float inv = row_ok ? a / lsum : 0.f;
-#pragma unroll
-  for (int e = 0; e < 12; ++e) sd[e] *= inv;
-#pragma unroll
-  for (int t = 0; t < kMaxSparse; ++t) ss[t] *= inv;
 
+  // ---- Dense P V: O^T = V^T P^T. ----
   f32x4_t accO[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) accO[db] = zero4();
 #pragma unroll
   for (int kk = 0; kk < 3; ++kk) {
-    const s16x4_t pb = pack_bf16x4(sd[4 * kk], sd[4 * kk + 1], sd[4 * kk + 2], sd[4 * kk + 3]);
+    const s16x4_t pb = pack_bf16x4(sd[4 * kk] * inv, sd[4 * kk + 1] * inv, sd[4 * kk + 2] * inv,
+                                   sd[4 * kk + 3] * inv);
     const bf16_t* vr = sV + (16 * w + 16 * kk + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
     for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vr + 16 * db), pb, accO[db]);
   }
 
-  // Long-range taps: V rows [n0 - delta, n0 - delta + 64) through a double-buffered LDS block.
-  uint4 stg[CH];
-  if (NS > 0) stage_rows<CH, CPR>(stg, vb, p.vs.n, n0 - p.taps.delta[W + 1], N, tid);
+  // ---- Long-range P V through the wave-private LDS block: O^T += V_t^T diag(p_t). ----
+  bf16_t* buf = sVs[w];
+  const bf16_t* vr = buf + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
-  for (int t = 0; t < kMaxSparse; ++t) {
-    if (t < NS) {
-      bf16_t* buf = sVs[t & 1];
+  for (int t = 0; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
 #pragma unroll
-      for (int cI = 0; cI < CH; ++cI) {
-        const int chunk = tid + cI * kBlock;
-        const int r = chunk / CPR, cc = chunk - r * CPR;
-        st16(buf + r * RV + cc * 8, stg[cI]);
+      for (int u = 0; u < CHW; ++u) {
+        const int ci = l + 64 * u;
+        st16(buf + (ci / CPR) * RV + (ci % CPR) * 8, vS[t % PF][u]);
       }
-      __syncthreads();
-      if (t + 1 < NS) stage_rows<CH, CPR>(stg, vb, p.vs.n, n0 - p.taps.delta[W + 2 + t], N, tid);
-      const float pt = ss[t];  // zero outside the diagonal lane
-      const int e = i & 3;
-      const s16x4_t bd = pack_bf16x4(e == 0 ? pt : 0.f, e == 1 ? pt : 0.f, e == 2 ? pt : 0.f,
-                                     e == 3 ? pt : 0.f);
-      const bf16_t* vr = buf + (16 * w + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+      if (t + PF < NS) {
+        const int r0 = n0w - p.taps.delta[W + 1 + t + PF];
+#pragma unroll
+        for (int u = 0; u < CHW; ++u) vS[t % PF][u] = bload16(rV, r0 * vsn + vlane[u]);
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the block is in LDS
+      __builtin_amdgcn_wave_barrier();
+      const s16x4_t bd = onehot_bf16x4(ss[t] * inv, i & 3);  // zero outside the diagonal lane
 #pragma unroll
       for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vr + 16 * db), bd, accO[db]);
     }
@@ -231,21 +264,37 @@ __global__ __launch_bounds__(kBlock) void fwd_mfma_kernel(FwdParams p) {
   }
 }
 
+template <int D, bool HAS_SE>
+static void launch_fwd_mfma_ns(const FwdParams& p, unsigned nblocks, hipStream_t st) {
+  // Long-range tap counts of the named tables (44, 46, 47 offsets) get fully unrolled kernels.
+  switch (p.taps.J - p.taps.W - 1) {
+    case 11: hipLaunchKernelGGL((fwd_mfma_kernel<D, HAS_SE, 11>), dim3(nblocks), dim3(kBlock), 0, st, p); break;
+    case 13: hipLaunchKernelGGL((fwd_mfma_kernel<D, HAS_SE, 13>), dim3(nblocks), dim3(kBlock), 0, st, p); break;
+    case 14: hipLaunchKernelGGL((fwd_mfma_kernel<D, HAS_SE, 14>), dim3(nblocks), dim3(kBlock), 0, st, p); break;
+    default: hipLaunchKernelGGL((fwd_mfma_kernel<D, HAS_SE, 0>), dim3(nblocks), dim3(kBlock), 0, st, p); break;
+  }
+}
+
 template <int D>
 static hipError_t launch_fwd_mfma_d(const FwdParams& p0, hipStream_t st) {
   FwdParams p = p0;
   p.n_tiles = (p.N + 63) / 64;
   const long long nblocks = (long long)p.B * p.H * p.n_tiles;
   if (nblocks == 0) return hipSuccess;
-  if (p.scale_embed)
-    hipLaunchKernelGGL((fwd_mfma_kernel<D, true>), dim3((unsigned)nblocks), dim3(kBlock), 0, st, p);
-  else
-    hipLaunchKernelGGL((fwd_mfma_kernel<D, false>), dim3((unsigned)nblocks), dim3(kBlock), 0, st, p);
+  if (p.scale_embed) launch_fwd_mfma_ns<D, true>(p, (unsigned)nblocks, st);
+  else launch_fwd_mfma_ns<D, false>(p, (unsigned)nblocks, st);
   return hipGetLastError();
 }
 
-bool fwd_mfma_supported(int D, const TapTable& t) {
-  return (D == 32 || D == 64 || D == 128) && t.J - t.W - 1 <= kMaxSparse;
+bool fwd_mfma_supported(const FwdParams& p, int D) {
+  // Buffer offsets are 32-bit: every row a tap can touch must stay below 2^31 bytes.
+  const long long rs = p.qs.n > p.ks.n ? (p.qs.n > p.vs.n ? p.qs.n : p.vs.n)
+                                        : (p.ks.n > p.vs.n ? p.ks.n : p.vs.n);
+  const long long rmin = p.qs.n < p.ks.n ? (p.qs.n < p.vs.n ? p.qs.n : p.vs.n)
+                                          : (p.ks.n < p.vs.n ? p.ks.n : p.vs.n);
+  const long long span = ((long long)p.N + p.taps.maxd + 64) * rs * 2;
+  return (D == 32 || D == 64 || D == 128) && p.taps.J - p.taps.W - 1 <= kMaxSparse &&
+         rmin >= D && span < (1LL << 31);
 }
 
 hipError_t launch_fwd_mfma(const FwdParams& p, int D, hipStream_t st) {

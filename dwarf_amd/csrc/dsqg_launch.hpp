@@ -9,14 +9,20 @@ namespace dsqg {
 // hipErrorInvalidValue for a head dim without a kernel (the ABI checks that first).
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, hipStream_t st);
 
-// bf16 MFMA forward (dsqg_fwd_mfma.hip): head dims 32/64/128 and at most kMaxSparse taps
-// beyond the dense window.  launch_fwd picks it whenever it applies.
-bool fwd_mfma_supported(int D, const TapTable& t);
+// bf16 MFMA forward (dsqg_fwd_mfma.hip): head dims 32/64/128, at most kMaxSparse taps beyond
+// the dense window, row strides >= D and 32-bit byte offsets within each (b,h) slice.
+// launch_fwd picks it whenever it applies.
+bool fwd_mfma_supported(const FwdParams& p, int D);
 hipError_t launch_fwd_mfma(const FwdParams& p, int D, hipStream_t st);
 
-// Tiling of the backward for these sizes; fills n_tiles / tiles_per_block / n_chunks.
-// With se_grad the dq workgroups cover more rows each, so fewer [J,D] partials are written.
-void bwd_plan(BwdParams& p, int D, bool se_grad);
+// Tiling of the backward for these sizes and kernel choice; fills n_tiles / tiles_per_block /
+// n_chunks / n_tiles_kv.  With se_grad the dq workgroups cover more rows each, so fewer [J,D]
+// partials are written.
+void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad);
+
+// bf16 MFMA backward kernels: same conditions as the MFMA forward.
+bool bwd_mfma_supported(const BwdParams& p, int D, int dtype);
+hipError_t launch_bwd_dq_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);

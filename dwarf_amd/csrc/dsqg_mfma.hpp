@@ -48,6 +48,36 @@ __device__ __forceinline__ uint2 pack_bf16x4_u2(float a, float b, float c, float
 
 __device__ __forceinline__ f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
 
+// Buffer resource over one (b,h) slice of a [B,H,N,D] bf16 operand: rows [0, N) of row stride rs
+// elements.  Raw buffer loads range-check each access against the slice size, so a row below 0
+// (negative 32-bit offset, i.e. a huge unsigned one) or at/after N reads as zeros -- the masked
+// taps cost no branch.  The caller guarantees (N + max offset) * rs * 2 < 2^31 and rs >= D.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const bf16_t* base, long long rs,
+                                                             int N, int D) {
+  const int bytes = N > 0 ? (int)(((long long)(N - 1) * rs + D) * 2) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, bytes,
+                                           0x00020000);
+}
+
+// 16 bytes at element offset `elem` of a buffer (zero when out of range).
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int elem) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (unsigned)(elem * 2), 0, 0));
+}
+
+// Hides a per-lane value from the optimiser, so that (uniform row) * stride + lane_part is not
+// re-associated into a per-lane (row + lane_row) * stride multiply (v_mul_lo_u32 is quarter rate).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// bf16 operand that holds x in element e (0..3) and zeros elsewhere.
+__device__ __forceinline__ s16x4_t onehot_bf16x4(float x, int e) {
+  const __bf16 hb = (__bf16)x;
+  const unsigned long long v = (unsigned long long)__builtin_bit_cast(unsigned short, hb) << (16 * e);
+  return __builtin_bit_cast(s16x4_t, v);
+}
+
 // Element r (runtime, 0..3) of a 4-vector without dynamic register indexing.
 __device__ __forceinline__ float pick4(f32x4_t v, int r) {
   const float lo = (r & 1) ? v[1] : v[0];
