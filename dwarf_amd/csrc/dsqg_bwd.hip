@@ -1,7 +1,7 @@
 // DSQG backward, launch 3 and the backward driver.
 //
 // bwd_reduce_kernel sums the per-workgroup parameter-gradient partials written by launch 1
-// (dsqg_bwd_dq.hip) in a fixed order, so dpos_bias / dscale_embed / dscore_gain / dif_gain are
+// (dsqg_bwd_dq.hip / dsqg_bwd_dq_mfma.hip) in a fixed order, so dpos_bias / dscale_embed / dscore_gain / dif_gain are
 // deterministic.  The reference accumulates dpb and dse with tl.atomic_add
 // (kernels/dsqg_attention_v3.py:265-271), whose summation order varies run to run.
 #include "dsqg_common.hpp"
@@ -9,19 +9,28 @@
 
 namespace dsqg {
 
-// One thread per parameter-gradient element; each sums its partials in a fixed order.
+// One wave per parameter-gradient element: lane l sums partials l, l+64, ... in order, then a
+// fixed xor-tree combines the lanes, so the result is the same on every run.
+__device__ __forceinline__ float wave_sum_fixed(float x) {
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) x += __shfl_xor(x, s, 64);
+  return x;
+}
+
 __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
-  const int i = blockIdx.x * kBlock + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  int t = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   const int JH = r.J * r.H;
-  const int per_h = r.B * r.n_chunks;
-  int t = i;
+  const int per_h = r.B * r.n_chunks;  // partials per head, ordered (b, chunk)
   if (t < JH) {  // dpos_bias[j,h]
     const int j = t / r.H, h = t - j * r.H;
     float s = 0.f;
-    for (int bb = 0; bb < r.B; ++bb)
-      for (int c = 0; c < r.n_chunks; ++c)
-        s += r.part_bias[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
-    r.dpos_bias[t] = s;
+    for (int k = lane; k < per_h; k += 64) {
+      const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
+      s += r.part_bias[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
+    }
+    s = wave_sum_fixed(s);
+    if (lane == 0) r.dpos_bias[t] = s;
     return;
   }
   t -= JH;
@@ -29,10 +38,12 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
     if (t < JH) {  // dscore_gain[h,j]
       const int h = t / r.J, j = t - h * r.J;
       float s = 0.f;
-      for (int bb = 0; bb < r.B; ++bb)
-        for (int c = 0; c < r.n_chunks; ++c)
-          s += r.part_gain[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
-      r.dscore_gain[t] = s;
+      for (int k = lane; k < per_h; k += 64) {
+        const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
+        s += r.part_gain[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
+      }
+      s = wave_sum_fixed(s);
+      if (lane == 0) r.dscore_gain[t] = s;
       return;
     }
     t -= JH;
@@ -40,10 +51,12 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
   if (r.dif_gain) {
     if (t < r.H) {
       float s = 0.f;
-      for (int bb = 0; bb < r.B; ++bb)
-        for (int c = 0; c < r.n_chunks; ++c)
-          s += r.part_if[(long long)(bb * r.H + t) * r.n_chunks + c];
-      r.dif_gain[t] = s;
+      for (int k = lane; k < per_h; k += 64) {
+        const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
+        s += r.part_if[(long long)(bb * r.H + t) * r.n_chunks + c];
+      }
+      s = wave_sum_fixed(s);
+      if (lane == 0) r.dif_gain[t] = s;
       return;
     }
     t -= r.H;
@@ -52,8 +65,9 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
     const long long nb = (long long)r.B * r.H * r.n_chunks;
     const long long stride = (long long)r.J * r.D;
     float s = 0.f;
-    for (long long blk = 0; blk < nb; ++blk) s += r.part_se[blk * stride + t];
-    r.dscale_embed[t] = s;
+    for (long long blk = lane; blk < nb; blk += 64) s += r.part_se[blk * stride + t];
+    s = wave_sum_fixed(s);
+    if (lane == 0) r.dscale_embed[t] = s;
   }
 }
 
@@ -68,8 +82,9 @@ bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
 }
 
 void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
-  const int QPB = bwd_mfma_supported(p, D, dtype) ? 64 : kBlock / (D / 8);
-  const int KPB = kBlock / (D / 8);  // dk/dv kernel rows per workgroup
+  const bool mfma = bwd_mfma_supported(p, D, dtype);
+  const int QPB = mfma ? 64 : kBlock / (D / 8);  // dq rows per tile
+  const int KPB = mfma ? 64 : kBlock / (D / 8);  // dk/dv rows per workgroup
   p.n_tiles = (p.N + QPB - 1) / QPB;
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
   const long long work = (long long)p.B * p.H * p.n_tiles;
@@ -82,9 +97,11 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
 }
 
 hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st) {
-  const long long total = 2LL * r.J * r.H + r.H + (long long)r.J * r.D;
+  const long long total = 2LL * r.J * r.H + r.H + (long long)r.J * r.D;  // outputs (upper bound)
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(bwd_reduce_kernel, dim3((unsigned)((total + kBlock - 1) / kBlock)), dim3(kBlock), 0, st, r);
+  const long long waves_per_block = kBlock / 64;
+  hipLaunchKernelGGL(bwd_reduce_kernel, dim3((unsigned)((total + waves_per_block - 1) / waves_per_block)),
+                     dim3(kBlock), 0, st, r);
   return hipGetLastError();
 }
 

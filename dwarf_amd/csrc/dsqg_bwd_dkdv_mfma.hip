@@ -1,0 +1,303 @@
+// DSQG backward, launch 2, bf16 MFMA path (gfx950): key-centric dk and dv.
+//
+// A workgroup owns one (b,h) and 64 key rows [m0, m0+64); wave w owns keys m0w = m0+16w .. +15.
+// Key m is read by the queries n = m + delta_j, so
+//   dv_m = sum_j a alpha_j(n) dOut_n,      dk_m = sum_j c g_j dS_j(n) q_n,
+//   alpha_j(n) = exp(s_j(n) - lse_n),      dS_j(n) = a alpha_j(n) (dOut_n . v_m - D'_n),
+// with lse from the forward and D' from launch 1.
+//  * Dense band: the wave's keys meet queries [m0w, m0w+48) in three 16x16 tiles
+//    S = Q K^T and U = dOut V^T (A = query rows, B = the wave's key / value rows).  In the MFMA
+//    result layout lane l holds key column l%16 and query rows 4*(l/16)+r, which is exactly the
+//    B operand of dK^T = Q^T (c g dS) and dV^T = dOut^T (a alpha); Q^T and dOut^T come from the
+//    query window [m0, m0+96) in LDS through ds_read_tr16_b64.
+//  * Long-range taps: query rows m0w + delta + 0..15 as the A operand; the wanted values sit on
+//    the diagonal (lane 16*(i/4)+i, register i%4).  Those query / dOut rows are staged in a
+//    wave-private LDS block for the transposed reads of the diagonal update.
+//  * The q.se_j term of the score (scale_embed) is a [query][tap] table per wave computed on the
+//    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps.
+// Follows _bwd_dkdv_v3 (kernels/dsqg_attention_v3.py:282-352).
+#include "dsqg_common.hpp"
+#include "dsqg_launch.hpp"
+#include "dsqg_mfma.hpp"
+
+namespace dsqg {
+
+template <int D, bool HAS_SE, int NSC>
+__global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
+  constexpr int KT = 64;                  // key rows per workgroup
+  constexpr int KS = D / 32;
+  constexpr int DB = D / 16;
+  constexpr int RV = D + 16;
+  constexpr int WIN = KT + kMaxWindow;    // query window rows [m0, m0+96)
+  constexpr int CPR = D / 8;
+  constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
+  constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
+  constexpr int PF = 2;
+  constexpr int TS = 52;                  // [query][tap] table row stride
+  constexpr int SEJ = 48;
+  constexpr float kLog2e = 1.4426950408889634f;
+
+  __shared__ __align__(16) bf16_t sQ[WIN * RV];
+  __shared__ __align__(16) bf16_t sO[WIN * RV];
+  __shared__ __align__(16) bf16_t sQs[4][16 * RV];   // wave-private long-range query rows
+  __shared__ __align__(16) bf16_t sOs[4][16 * RV];   // ... and their dOut rows
+  __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
+  __shared__ float sT[HAS_SE ? WIN * TS : 1];        // log2e (bias + c q.se) per window query, tap
+  __shared__ float sBias2[kMaxTaps];
+  __shared__ float sGain2[kMaxTaps];                 // gain * c * log2e
+  __shared__ float sGainC[kMaxTaps];                 // gain * c
+
+  const int tid = threadIdx.x;
+  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  const int bh = lb / p.n_tiles_kv, tile = lb - bh * p.n_tiles_kv;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int N = p.N, J = p.taps.J, W = p.taps.W;
+  const int NS = NSC > 0 ? NSC : J - W - 1;
+  const float c = p.scale, c2 = p.scale * kLog2e;
+  const float a = p.if_gain ? p.if_gain[h] : 1.0f;
+  const int qsn = (int)p.qs.n, ksn = (int)p.ks.n, vsn = (int)p.vs.n, dosn = (int)p.dos.n;
+  const int m0 = tile * KT;
+  const long long rowbase = ((long long)b * p.H + h) * N;
+
+  const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rK = slice_rsrc(static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h, p.ks.n, N, D);
+  const __amdgpu_buffer_rsrc_t rV = slice_rsrc(static_cast<const bf16_t*>(p.v) + b * p.vs.b + h * p.vs.h, p.vs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rO = slice_rsrc(static_cast<const bf16_t*>(p.dout) + b * p.dos.b + h * p.dos.h, p.dos.n, N, D);
+  const __amdgpu_buffer_rsrc_t rL = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.lse + rowbase), (short)0, N * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rP = __builtin_amdgcn_make_buffer_rsrc(p.dpre + rowbase, (short)0, N * 4, 0x00020000);
+
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 15, g = l >> 4;
+  const int m0w = m0 + 16 * w;
+  const int m = m0w + i;                  // key row of this lane's MFMA column
+  const bool key_ok = m < N;
+  const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
+  const int klane = opaque(i * ksn + 8 * g), vlane = opaque(i * vsn + 8 * g);
+
+  // ---- Loads. ----
+  uint4 wq[CWIN], wo[CWIN];
+#pragma unroll
+  for (int u = 0; u < CWIN; ++u) {
+    const int ci = tid + u * kBlock;
+    wq[u] = bload16(rQ, m0 * qsn + opaque((ci / CPR) * qsn + (ci % CPR) * 8));
+    wo[u] = bload16(rO, m0 * dosn + opaque((ci / CPR) * dosn + (ci % CPR) * 8));
+  }
+  bf16x8_t kB[KS], vB[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kB[s] = as_bf16x8(bload16(rK, m0w * ksn + klane + 32 * s));
+    vB[s] = as_bf16x8(bload16(rV, m0w * vsn + vlane + 32 * s));
+  }
+  // lse (log2 units) and D' of the band's queries m0w + 16qb + 4g + r.
+  float lq[12], dq_[12];
+#pragma unroll
+  for (int qb = 0; qb < 3; ++qb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int nq = m0w + 16 * qb + 4 * g + r;
+      lq[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
+      dq_[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
+    }
+  uint4 qS[PF][KS], oS[PF][KS];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) {
+    if (t < NS) {
+      const int n0 = m0w + p.taps.delta[W + 1 + t];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        qS[t][s] = bload16(rQ, n0 * qsn + qlane + 32 * s);
+        oS[t][s] = bload16(rO, n0 * dosn + olane + 32 * s);
+      }
+    }
+  }
+
+  for (int j = tid; j < J; j += kBlock) {
+    const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
+    sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
+    sGain2[j] = gj * c2;
+    sGainC[j] = gj * c;
+  }
+  if constexpr (HAS_SE) {
+    for (int e = tid; e < SEJ * D; e += kBlock) {
+      const int j = e / D, d = e - j * D;
+      const float x = j < J ? p.scale_embed[j * D + d] : 0.f;
+      sSE[j * RV + d] = __builtin_bit_cast(bf16_t, (__bf16)x);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < CWIN; ++u) {
+    const int ci = tid + u * kBlock;
+    if (ci < WIN * CPR) {
+      st16(sQ + (ci / CPR) * RV + (ci % CPR) * 8, wq[u]);
+      st16(sO + (ci / CPR) * RV + (ci % CPR) * 8, wo[u]);
+    }
+  }
+  __syncthreads();
+
+  // ---- Dense band: S = Q K^T, U = dOut V^T for query blocks qb = 0..2. ----
+  f32x4_t accS[3], accU[3];
+#pragma unroll
+  for (int qb = 0; qb < 3; ++qb) {
+    accS[qb] = zero4();
+    accU[qb] = zero4();
+    const bf16_t* qr = sQ + (16 * w + 16 * qb + i) * RV + 8 * g;
+    const bf16_t* orr = sO + (16 * w + 16 * qb + i) * RV + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      accS[qb] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * s)), kB[s], accS[qb]);
+      accU[qb] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(orr + 32 * s)), vB[s], accU[qb]);
+    }
+  }
+  if constexpr (HAS_SE) {
+    // T[row][j] = log2e (bias_j + c q.se_j) for the 96 window queries (Q SE^T), 16-row blocks
+    // w and w+4 per wave.
+    for (int blk = w; blk < WIN / 16; blk += 4) {
+      const bf16_t* qr = sQ + (16 * blk + i) * RV + 8 * g;
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        f32x4_t acc = zero4();
+        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * s)),
+                              as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), acc);
+        const int j = 16 * jb + i;  // column = tap, rows = queries 4g + r
+        if (j < J) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sT[(16 * blk + 4 * g + r) * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  f32x4_t dK[DB], dV[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) { dK[db] = zero4(); dV[db] = zero4(); }
+#pragma unroll
+  for (int qb = 0; qb < 3; ++qb) {
+    float wk[4], wv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int dl = 16 * qb + 4 * g + r - i;  // query - key
+      const int nq = m0w + 16 * qb + 4 * g + r;
+      const bool ok = key_ok && (unsigned)dl <= (unsigned)W && nq < N;
+      const int j = ok ? dl : 0;
+      const float s2 = fmaf(sGain2[j], accS[qb][r],
+                            HAS_SE ? sT[(16 * w + 16 * qb + 4 * g + r) * TS + j] : sBias2[j]);
+      const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lq[4 * qb + r]) : 0.f;
+      const float dS = a * alpha * (accU[qb][r] - dq_[4 * qb + r]);
+      wk[r] = sGainC[j] * dS;
+      wv[r] = a * alpha;
+    }
+    const s16x4_t bk = pack_bf16x4(wk[0], wk[1], wk[2], wk[3]);
+    const s16x4_t bv = pack_bf16x4(wv[0], wv[1], wv[2], wv[3]);
+    const bf16_t* qr = sQ + (16 * w + 16 * qb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+    const bf16_t* orr = sO + (16 * w + 16 * qb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      dK[db] = mfma_16x16x16(lds_read_tr16(qr + 16 * db), bk, dK[db]);
+      dV[db] = mfma_16x16x16(lds_read_tr16(orr + 16 * db), bv, dV[db]);
+    }
+  }
+
+  // ---- Long-range taps: queries m0w + delta + 0..15, diagonal of one tile each. ----
+  const bool diag = g == (i >> 2);
+  bf16_t* qsw = sQs[w];
+  bf16_t* osw = sOs[w];
+  const bf16_t* qtr = qsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+  const bf16_t* otr = osw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+  for (int t = 0; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
+      const int j = W + 1 + t;
+      const int dl = p.taps.delta[j];
+      f32x4_t as = zero4(), au = zero4();
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        as = mfma_16x16x32(as_bf16x8(qS[t % PF][s]), kB[s], as);
+        au = mfma_16x16x32(as_bf16x8(oS[t % PF][s]), vB[s], au);
+      }
+      float tq;  // log2e (bias + c q.se) for query row i of this block
+      if constexpr (HAS_SE) {
+        float part = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const bf16x8_t qv = as_bf16x8(qS[t % PF][s]);
+          const bf16x8_t sv = *reinterpret_cast<const bf16x8_t*>(sSE + j * RV + 32 * s + 8 * g);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) part = fmaf((float)qv[e], (float)sv[e], part);
+        }
+        tq = fmaf(c2, col_sum(part), sBias2[j]);
+      } else {
+        tq = sBias2[j];
+      }
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        st16(qsw + i * RV + 8 * g + 32 * s, qS[t % PF][s]);
+        st16(osw + i * RV + 8 * g + 32 * s, oS[t % PF][s]);
+      }
+      if (t + PF < NS) {
+        const int n0 = m0w + p.taps.delta[W + 1 + t + PF];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          qS[t % PF][s] = bload16(rQ, n0 * qsn + qlane + 32 * s);
+          oS[t % PF][s] = bload16(rO, n0 * dosn + olane + 32 * s);
+        }
+      }
+      const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
+      const float lseq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
+      const float dpq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
+      const bool ok = diag && key_ok && nq < N;
+      const float raw = pick4(as, i & 3), uval = pick4(au, i & 3);
+      const float alpha = ok ? __builtin_amdgcn_exp2f(fmaf(sGain2[j], raw, tq) - lseq) : 0.f;
+      const float dS = a * alpha * (uval - dpq);
+      const s16x4_t bk = onehot_bf16x4(sGainC[j] * dS, i & 3);
+      const s16x4_t bv = onehot_bf16x4(a * alpha, i & 3);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        dK[db] = mfma_16x16x16(lds_read_tr16(qtr + 16 * db), bk, dK[db]);
+        dV[db] = mfma_16x16x16(lds_read_tr16(otr + 16 * db), bv, dV[db]);
+      }
+    }
+  }
+
+  if (key_ok) {
+    bf16_t* dkr = static_cast<bf16_t*>(p.dk) + b * p.dks.b + h * p.dks.h + m * p.dks.n + 4 * g;
+    bf16_t* dvr = static_cast<bf16_t*>(p.dv) + b * p.dvs.b + h * p.dvs.h + m * p.dvs.n + 4 * g;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      *reinterpret_cast<uint2*>(dkr + 16 * db) = pack_bf16x4_u2(dK[db][0], dK[db][1], dK[db][2], dK[db][3]);
+      *reinterpret_cast<uint2*>(dvr + 16 * db) = pack_bf16x4_u2(dV[db][0], dV[db][1], dV[db][2], dV[db][3]);
+    }
+  }
+}
+
+template <int D, bool HAS_SE>
+static void launch_dkdv_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
+  switch (p.taps.J - p.taps.W - 1) {
+    case 11: hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<D, HAS_SE, 11>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 13: hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<D, HAS_SE, 13>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 14: hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<D, HAS_SE, 14>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    default: hipLaunchKernelGGL((bwd_dkdv_mfma_kernel<D, HAS_SE, 0>), dim3(nb), dim3(kBlock), 0, st, p); break;
+  }
+}
+
+template <int D>
+static hipError_t launch_dkdv_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
+  if (p.scale_embed) launch_dkdv_mfma_ns<D, true>(p, nb, st);
+  else launch_dkdv_mfma_ns<D, false>(p, nb, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd_dkdv_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st) {
+  switch (D) {
+    case 32: return launch_dkdv_mfma_d<32>(p, nblocks, st);
+    case 64: return launch_dkdv_mfma_d<64>(p, nblocks, st);
+    case 128: return launch_dkdv_mfma_d<128>(p, nblocks, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace dsqg

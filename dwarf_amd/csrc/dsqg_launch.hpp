@@ -23,6 +23,7 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad);
 // bf16 MFMA backward kernels: same conditions as the MFMA forward.
 bool bwd_mfma_supported(const BwdParams& p, int D, int dtype);
 hipError_t launch_bwd_dq_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st);
+hipError_t launch_bwd_dkdv_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
