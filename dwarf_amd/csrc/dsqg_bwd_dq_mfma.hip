@@ -40,7 +40,8 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int SE_PER_T = (SEJ * D + kBlock - 1) / kBlock;
   constexpr float kLog2e = 1.4426950408889634f;
 
-  __shared__ __align__(16) bf16_t sK[WIN * RV];        // dense-window K rows (transposing reads)
+  __shared__ __align__(16) bf16_t sK[WIN * RV];        // dense-window K rows
+  __shared__ __align__(16) bf16_t sV[WIN * RV];        // dense-window V rows
   __shared__ __align__(16) bf16_t sKs[4][16 * RV];     // wave-private long-range K block
   __shared__ __align__(16) bf16_t sQ[HAS_SE ? 4 * 16 * RV : 8];   // wave's Q rows (for dse)
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];     // scale_embed rows, bf16
@@ -116,26 +117,20 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
     const bool row_ok = n < N;
 
     // ---- Loads (zero outside [0, N)). ----
-    uint4 wk[CWIN];
+    // Dense window K and V rows [n0-32, n0+64), staged once per workgroup in LDS.
+    uint4 wk[CWIN], wv[CWIN];
 #pragma unroll
     for (int u = 0; u < CWIN; ++u) {
       const int ci = tid + u * kBlock;
       wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque((ci / CPR) * ksn + (ci % CPR) * 8));
+      wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque((ci / CPR) * vsn + (ci % CPR) * 8));
     }
     bf16x8_t qB[KS], oB[KS];
-    uint4 kD[3][KS], vD[3][KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
       oB[s] = as_bf16x8(bload16(rO, n0w * dosn + olane + 32 * s));
     }
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk)
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        kD[kk][s] = bload16(rK, (n0w - 32 + 16 * kk) * ksn + klane + 32 * s);
-        vD[kk][s] = bload16(rV, (n0w - 32 + 16 * kk) * vsn + vlane + 32 * s);
-      }
     const float lse2 = row_ok ? p.lse[rowbase + n] * kLog2e : 0.f;
     uint4 kS[PF][KS], vS[PF][KS];
 #pragma unroll
@@ -154,7 +149,10 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
 #pragma unroll
     for (int u = 0; u < CWIN; ++u) {
       const int ci = tid + u * kBlock;
-      if (ci < WIN * CPR) st16(sK + (ci / CPR) * RV + (ci % CPR) * 8, wk[u]);
+      if (ci < WIN * CPR) {
+        st16(sK + (ci / CPR) * RV + (ci % CPR) * 8, wk[u]);
+        st16(sV + (ci / CPR) * RV + (ci % CPR) * 8, wv[u]);
+      }
     }
     if constexpr (HAS_SE) {
       // The wave's Q rows (B layout: row i, chunks 8g + 32s) as natural rows, for dse.
@@ -170,10 +168,12 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
     for (int kk = 0; kk < 3; ++kk) {
       accS[kk] = zero4();
       accU[kk] = zero4();
+      const bf16_t* kr = sK + (16 * w + 16 * kk + i) * RV + 8 * g;
+      const bf16_t* vr = sV + (16 * w + 16 * kk + i) * RV + 8 * g;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        accS[kk] = mfma_16x16x32(as_bf16x8(kD[kk][s]), qB[s], accS[kk]);
-        accU[kk] = mfma_16x16x32(as_bf16x8(vD[kk][s]), oB[s], accU[kk]);
+        accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
+        accU[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(vr + 32 * s)), oB[s], accU[kk]);
       }
     }
     if constexpr (HAS_SE) {

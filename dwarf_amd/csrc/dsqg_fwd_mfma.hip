@@ -44,6 +44,7 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sV[WIN * RV];
+  __shared__ __align__(16) bf16_t sK[WIN * RV];   // dense-window K rows (MFMA A operands)
   __shared__ __align__(16) bf16_t sVs[4][16 * RV];   // wave-private long-range V block
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
   __shared__ float sT[HAS_SE ? 4 * 16 * TS : 1];
@@ -72,21 +73,17 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
 
   // ---- Global loads (all zero-filled outside [0, N) by the buffer range check). ----
   // Offsets are (uniform row) * stride + (per-lane part), so the row products stay scalar.
-  uint4 wv[CWIN];
+  uint4 wv[CWIN], wk[CWIN];
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
     wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque((ci / CPR) * vsn + (ci % CPR) * 8));
+    wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque((ci / CPR) * ksn + (ci % CPR) * 8));
   }
   const int qlane = opaque(i * qsn + 8 * g), klane = opaque(i * ksn + 8 * g);
   bf16x8_t qB[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
-  uint4 kD[3][KS];   // dense band: key rows n0w-32+16kk+i as A operands
-#pragma unroll
-  for (int kk = 0; kk < 3; ++kk)
-#pragma unroll
-    for (int s = 0; s < KS; ++s) kD[kk][s] = bload16(rK, (n0w - 32 + 16 * kk) * ksn + klane + 32 * s);
   // Long-range key rows n0w - delta + i, loaded in two halves (the second after the dense band
   // has consumed its registers) to bound the register peak.
   constexpr int NH = (NSM + 1) / 2;
@@ -114,7 +111,10 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
     const int r = ci / CPR, cc = ci - r * CPR;
-    if (ci < WIN * CPR) st16(sV + r * RV + cc * 8, wv[u]);
+    if (ci < WIN * CPR) {
+      st16(sV + r * RV + cc * 8, wv[u]);
+      st16(sK + r * RV + cc * 8, wk[u]);
+    }
   }
   __syncthreads();
 
@@ -123,8 +123,10 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
 #pragma unroll
   for (int kk = 0; kk < 3; ++kk) {
     accS[kk] = zero4();
+    const bf16_t* kr = sK + (16 * w + 16 * kk + i) * RV + 8 * g;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) accS[kk] = mfma_16x16x32(as_bf16x8(kD[kk][s]), qB[s], accS[kk]);
+    for (int s = 0; s < KS; ++s)
+      accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
