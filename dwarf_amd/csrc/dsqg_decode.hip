@@ -7,9 +7,9 @@
 // written, so the write and the reads of one step never touch the same row.
 //
 // One wave64 per (b,h), four per workgroup.  Lanes form R = 64/G groups of G = D/8 lanes; in
-// pass t group r handles tap j = t*R + r, so the J key rows (and then the J value rows) are
-// fetched as R coalesced rows at a time with all passes' loads in flight together.  The
-// softmax max/sum and the output sum across groups use cross-lane shuffles.
+// pass t group r handles tap j = t*R + r, so the J key and value rows are fetched as R
+// coalesced rows at a time, all of them requested before any arithmetic.  The softmax max/sum
+// and the output sum across groups use DPP and v_permlane16/32_swap (no LDS).
 //
 // The reference has no decode kernel (train/train_2048_condU.py:463-487 recomputes the prefix);
 // the ring follows README.md:175-177.
@@ -18,17 +18,30 @@
 
 namespace dsqg {
 
+// Combine the R lane groups of G = 64/R lanes (lanes l, l^G, l^2G, ...): xor 8 inside a
+// 16-lane row by DPP row_ror:8, xor 16 / xor 32 by v_permlane16/32_swap.  Every lane ends with
+// the total; the pairing order is the same on both lanes of each pair.
 template <int R>
-__device__ __forceinline__ float cross_group_max(float x, int G) {
-#pragma unroll
-  for (int s = 1; s < R; s <<= 1) x = fmaxf(x, __shfl_xor(x, s * G, 64));
-  return x;
+__device__ __forceinline__ float groups_reduce_sum(float x) {
+  constexpr int G = 64 / R;
+  if constexpr (G <= 8) x += dpp_f32<0x128>(x);                           // lane ^ 8
+  if constexpr (G <= 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(r[0]) + __uint_as_float(r[1]);                    // lane ^ 16
+  }
+  const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r2[0]) + __uint_as_float(r2[1]);                 // lane ^ 32
 }
 template <int R>
-__device__ __forceinline__ float cross_group_sum(float x, int G) {
-#pragma unroll
-  for (int s = 1; s < R; s <<= 1) x += __shfl_xor(x, s * G, 64);
-  return x;
+__device__ __forceinline__ float groups_reduce_max(float x) {
+  constexpr int G = 64 / R;
+  if constexpr (G <= 8) x = fmaxf(x, dpp_f32<0x128>(x));
+  if constexpr (G <= 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r2[0]), __uint_as_float(r2[1]));
 }
 
 template <typename T, int D, int JMAX, bool HAS_SE>
@@ -64,48 +77,45 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
   T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
 
+  // Every K and V row of this lane group's taps is requested before any arithmetic: one memory
+  // round trip per step.  Masked taps (pos - delta < 0) read a valid slot and are zeroed.
   float q[8];
   Vec8<T>::load(qrow + d0, q);
-
-  float s[P];
-  int slot[P];
+  float kx[P][8], vx[P][8];
+  bool ok[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const int j = t * R + r;
-    float part = 0.f, bias = 0.f;
-    bool ok = false;
-    slot[t] = -1;
-    if (j < J) {
-      const int dl = p.taps.delta[j];
-      ok = pos - dl >= 0;
-      bias = p.pos_bias[j * p.H + h];
-      if (ok) {
-        float kx[8];
-        if (dl == 0) {
-          Vec8<T>::load(knew + d0, kx);
-        } else {
-          long long sl = (pos - dl) % S;
-          slot[t] = (int)sl;
-          Vec8<T>::load(kring + sl * D + d0, kx);
-        }
-        float pk = 0.f;
+    const int dl = j < J ? p.taps.delta[j] : 0;
+    ok[t] = j < J && pos - dl >= 0;
+    const long long sl = ok[t] ? (pos - dl) % S : 0;
+    const T* ks = dl == 0 ? knew : kring + sl * D;
+    const T* vs = dl == 0 ? vnew : vring + sl * D;
+    Vec8<T>::load(ks + d0, kx[t]);
+    Vec8<T>::load(vs + d0, vx[t]);
+  }
+
+  float s[P];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[e], pk);
-        part = pk * (p.score_gain ? p.score_gain[h * J + j] : 1.0f);
-        if constexpr (HAS_SE) {
+  for (int t = 0; t < P; ++t) {
+    const int j = t * R + r;
+    const int jj = j < J ? j : 0;
+    float pk = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[j * D + d0 + e], part);
-        }
-      }
+    for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[t][e], pk);
+    float part = pk * (p.score_gain ? p.score_gain[h * J + jj] : 1.0f);
+    if constexpr (HAS_SE) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[jj * D + d0 + e], part);
     }
     const float tot = group_sum<G>(part);
-    s[t] = ok ? fmaf(tot, c, bias) : -INFINITY;
+    s[t] = ok[t] ? fmaf(tot, c, p.pos_bias[jj * p.H + h]) : -INFINITY;
   }
 
   float mx = -INFINITY;
 #pragma unroll
   for (int t = 0; t < P; ++t) mx = fmaxf(mx, s[t]);
-  mx = cross_group_max<R>(mx, G);
+  mx = groups_reduce_max<R>(mx);
 
   float l = 0.f, acc[8];
 #pragma unroll
@@ -114,18 +124,12 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   for (int t = 0; t < P; ++t) {
     const float pj = __expf(s[t] - mx);
     l += pj;
-    const int j = t * R + r;
-    if (j < J && s[t] != -INFINITY) {
-      float vx[8];
-      if (slot[t] < 0) Vec8<T>::load(vnew + d0, vx);
-      else Vec8<T>::load(vring + (long long)slot[t] * D + d0, vx);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, vx[e], acc[e]);
-    }
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, ok[t] ? vx[t][e] : 0.f, acc[e]);
   }
-  l = cross_group_sum<R>(l, G);
+  l = groups_reduce_sum<R>(l);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = cross_group_sum<R>(acc[e], G);
+  for (int e = 0; e < 8; ++e) acc[e] = groups_reduce_sum<R>(acc[e]);
 
   if (r == 0) {
     const float a = p.if_gain ? p.if_gain[h] : 1.0f;
