@@ -97,6 +97,17 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
       lq[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
       dq_[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
     }
+  // lse and D' of the query on this lane's diagonal for every long-range tap (query m + delta;
+  // lanes off the diagonal fetch a harmless value), requested before the tap loop.
+  float lseS[NSM], dpS[NSM];
+#pragma unroll
+  for (int t = 0; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
+      const int nq = m + p.taps.delta[W + 1 + t];
+      lseS[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
+      dpS[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
+    }
+  }
   uint4 qS[PF][KS], oS[PF][KS];
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
@@ -245,8 +256,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
         }
       }
       const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
-      const float lseq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
-      const float dpq = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
+      const float lseq = lseS[t], dpq = dpS[t];
       const bool ok = diag && key_ok && nq < N;
       const float raw = pick4(as, i & 3), uval = pick4(au, i & 3);
       const float alpha = ok ? __builtin_amdgcn_exp2f(fmaf(sGain2[j], raw, tq) - lseq) : 0.f;
