@@ -7,9 +7,12 @@
 //     LDS, B = the wave's query rows, straight from global memory).  Lane l then holds query
 //     column i = l%16 and keys 4*(l/16) + r of each 16-key block, i.e. delta = n - m is known
 //     per register; taps outside delta in [0, W] (or before row 0) become -inf.
-//  3. Long-range taps: for tap delta the key rows are the contiguous block n0w - delta + 0..15;
-//     S^T_t = K_t Q^T is one 16x16 tile whose diagonal holds the 16 wanted scores (lane
-//     16*(i/4) + i, register i%4).  The K rows are coalesced 16-byte loads from L2.
+//  3. Long-range taps: for tap delta the key rows are the contiguous block n0w - delta + 0..15.
+//     They are loaded whole-row (8 lanes x 16 bytes per 128-byte row for D=64) and dotted with
+//     the query rows on the VALU (v_dot2_f32_bf16, DPP sum over the row's lanes); the 16 scores
+//     go through a per-wave LDS table to the lane that owns query i's taps.  An MFMA diagonal
+//     would need the operand order (16 rows x 16 bytes per 16 lanes), which the vector L1
+//     serves at about a quarter of the whole-row rate.
 //  4. Optional q.se_j term: SE Q^T with the same MFMA, kept per wave in an LDS table
 //     T[i][j] = bias[j] + c q_i . se_j; without scale_embed T is the bias row.
 //  5. Softmax over each query's J taps in registers: the four lanes of a query column combine
@@ -48,6 +51,7 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
   __shared__ __align__(16) bf16_t sVs[4][16 * RV];   // wave-private long-range V block
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
   __shared__ float sT[HAS_SE ? 4 * 16 * TS : 1];
+  __shared__ __align__(16) float sRaw[4][16 * 16];   // per wave: long-range q.k [query][tap]
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
 
@@ -80,20 +84,30 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
     wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque((ci / CPR) * vsn + (ci % CPR) * 8));
     wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque((ci / CPR) * ksn + (ci % CPR) * 8));
   }
-  const int qlane = opaque(i * qsn + 8 * g), klane = opaque(i * ksn + 8 * g);
+  const int qlane = opaque(i * qsn + 8 * g);
   bf16x8_t qB[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
-  // Long-range key rows n0w - delta + i, loaded in two halves (the second after the dense band
-  // has consumed its registers) to bound the register peak.
+  // The same query rows and the long-range key rows n0w - delta + 0..15 in the row-chunk
+  // layout (whole rows per 8 lanes); the keys in two halves (the second after the dense band has
+  // consumed its registers) to bound the register peak.
+  int qlaneR[CHW], klaneR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    qlaneR[u] = opaque(rc_row<D>(l, u) * qsn + rc_chunk<D>(l, u) * 8);
+    klaneR[u] = opaque(rc_row<D>(l, u) * ksn + rc_chunk<D>(l, u) * 8);
+  }
+  uint4 qR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
   constexpr int NH = (NSM + 1) / 2;
-  uint4 kS[NSM][KS];
+  uint4 kS[NSM][CHW];
 #pragma unroll
   for (int t = 0; t < NH; ++t) {
     if (NSC > 0 || t < NS) {
       const int m0 = n0w - p.taps.delta[W + 1 + t];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kS[t][s] = bload16(rK, m0 * ksn + klane + 32 * s);
+      for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
     }
   }
   for (int j = tid; j < J; j += kBlock) {
@@ -129,17 +143,31 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
       accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // Long-range q.k on the VALU: each lane dots its 16-byte chunk, the CPR lanes of a row sum
+  // (DPP), and one lane per row files the score in the wave's [query][tap] table.  The first
+  // half's registers are free before the second half is loaded.
+  float* sRw = sRaw[w];
+#pragma unroll
+  for (int t = 0; t < NH; ++t) {
+    if (NSC > 0 || t < NS) {
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        const float d = group_sum<CPR>(dot8_bf16(qR[u], kS[t][u], 0.f));
+        if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * 16 + t] = d;
+      }
+    }
+  }
 #pragma unroll
   for (int t = NH; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
       const int m0 = n0w - p.taps.delta[W + 1 + t];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kS[t][s] = bload16(rK, m0 * ksn + klane + 32 * s);
+      for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
     }
   }
-  int vlane[CHW];  // this lane's chunks of a wave's 16-row V block
+  int vlane[CHW];  // this lane's chunks of a wave's 16-row V block (row-chunk layout)
 #pragma unroll
-  for (int u = 0; u < CHW; ++u) vlane[u] = opaque(((l + 64 * u) / CPR) * vsn + ((l + 64 * u) % CPR) * 8);
+  for (int u = 0; u < CHW; ++u) vlane[u] = opaque(rc_row<D>(l, u) * vsn + rc_chunk<D>(l, u) * 8);
   uint4 vS[PF][CHW];  // long-range V rows n0w - delta + 0..15, PF taps ahead
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
@@ -186,6 +214,20 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
     }
   }
 
+#pragma unroll
+  for (int t = NH; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        const float d = group_sum<CPR>(dot8_bf16(qR[u], kS[t][u], 0.f));
+        if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * 16 + t] = d;
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the table is written
+  __builtin_amdgcn_wave_barrier();
+  // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the
+  // one-hot P operand of the long-range P V below must sit there.
   const bool diag = g == (i >> 2);
   float ss[NSM];
 #pragma unroll
@@ -193,10 +235,7 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
     ss[t] = -INFINITY;
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      f32x4_t acc = zero4();
-#pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mfma_16x16x32(as_bf16x8(kS[t][s]), qB[s], acc);
-      const float v = fmaf(sGain2[j], pick4(acc, i & 3), HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+      const float v = fmaf(sGain2[j], sRw[i * 16 + t], HAS_SE ? sTw[i * TS + j] : sBias2[j]);
       ss[t] = (diag && row_ok && n >= p.taps.delta[j]) ? v : -INFINITY;
     }
   }

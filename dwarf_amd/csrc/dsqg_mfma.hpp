@@ -48,6 +48,26 @@ __device__ __forceinline__ uint2 pack_bf16x4_u2(float a, float b, float c, float
 
 __device__ __forceinline__ f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
 
+// acc + a . b over eight bf16 pairs (v_dot2_f32_bf16: exact products, fp32 accumulation).
+__device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.x), __builtin_bit_cast(bf16x2_t, b.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.y), __builtin_bit_cast(bf16x2_t, b.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.z), __builtin_bit_cast(bf16x2_t, b.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a.w), __builtin_bit_cast(bf16x2_t, b.w), acc, false);
+  return acc;
+}
+
+// Row-chunk layout of a wave's 16-row block of a [rows][D] bf16 matrix: load u (0 .. D/32-1)
+// gives lane l the 16-byte chunk (l + 64u) % (D/8) of row (l + 64u) / (D/8).  Eight (D=64)
+// consecutive lanes then read one whole 128-byte row, which the vector L1 serves at close to
+// four times the rate of the MFMA operand order (16 rows x 16 bytes per 16 lanes), where every
+// group of four lanes touches four different cache lines.
+template <int D>
+__device__ __forceinline__ int rc_row(int l, int u) { return (l + 64 * u) / (D / 8); }
+template <int D>
+__device__ __forceinline__ int rc_chunk(int l, int u) { return (l + 64 * u) % (D / 8); }
+
 // Buffer resource over one (b,h) slice of a [B,H,N,D] bf16 operand: rows [0, N) of row stride rs
 // elements.  Raw buffer loads range-check each access against the slice size, so a row below 0
 // (negative 32-bit offset, i.e. a huge unsigned one) or at/after N reads as zeros -- the masked
