@@ -33,6 +33,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int WIN = QT + kMaxWindow;
   constexpr int CPR = D / 8;
   constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
+  constexpr int CHW = D / 32;             // 16-byte chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;                   // long-range K/V operands loaded ahead of use
   constexpr int TS = 52;                  // row stride of the per-wave [query][tap] tables (16 B aligned)
@@ -52,6 +53,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   __shared__ float sGain2[kMaxTaps];                    // gain * c * log2e
   __shared__ float sGain[kMaxTaps];
   __shared__ float sDp[4 * 16];
+  __shared__ float2 sPair[4][16];                       // per wave: long-range (q.k, dOut.v) of one tap
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -72,8 +74,16 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   const long long rowbase = ((long long)b * p.H + h) * N;
 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 15, g = l >> 4;
-  const int qlane = opaque(i * qsn + 8 * g), klane = opaque(i * ksn + 8 * g);
-  const int vlane = opaque(i * vsn + 8 * g), olane = opaque(i * dosn + 8 * g);
+  const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
+  // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
+  int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    qlaneR[u] = opaque(rc_row<D>(l, u) * qsn + rc_chunk<D>(l, u) * 8);
+    olaneR[u] = opaque(rc_row<D>(l, u) * dosn + rc_chunk<D>(l, u) * 8);
+    klaneR[u] = opaque(rc_row<D>(l, u) * ksn + rc_chunk<D>(l, u) * 8);
+    vlaneR[u] = opaque(rc_row<D>(l, u) * vsn + rc_chunk<D>(l, u) * 8);
+  }
 
   for (int j = tid; j < J; j += kBlock) {
     const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
@@ -131,16 +141,23 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
       qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
       oB[s] = as_bf16x8(bload16(rO, n0w * dosn + olane + 32 * s));
     }
+    uint4 qR[CHW], oR[CHW];
+#pragma unroll
+    for (int u = 0; u < CHW; ++u) {
+      qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
+      oR[u] = bload16(rO, n0w * dosn + olaneR[u]);
+    }
     const float lse2 = row_ok ? p.lse[rowbase + n] * kLog2e : 0.f;
-    uint4 kS[PF][KS], vS[PF][KS];
+    // Long-range K/V rows n0w - delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
+    uint4 kS[PF][CHW], vS[PF][CHW];
 #pragma unroll
     for (int t = 0; t < PF; ++t) {
       if (t < NS) {
         const int m0 = n0w - p.taps.delta[W + 1 + t];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          kS[t][s] = bload16(rK, m0 * ksn + klane + 32 * s);
-          vS[t][s] = bload16(rV, m0 * vsn + vlane + 32 * s);
+        for (int u = 0; u < CHW; ++u) {
+          kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
+          vS[t][u] = bload16(rV, m0 * vsn + vlaneR[u]);
         }
       }
     }
@@ -212,6 +229,8 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
         uu[4 * kk + r] = accU[kk][r];
         dlane = fmaf(alpha, accU[kk][r], dlane);
         wlane += alpha;
+        // c q.k for dg goes to the table now (frees the score registers for the taps loop).
+        if ((unsigned)dl <= (unsigned)W) sRAWw[i * TS + dl] = c * accS[kk][r];
       }
     }
     const float wsum = col_sum(wlane);
@@ -242,43 +261,45 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
 
     // ---- Long-range taps (diagonal of one 16x16 tile each). ----
     const bool diag = g == (i >> 2);
-    float als[NSM], uus[NSM], raws[NSM];
+    float als[NSM], uus[NSM];
     const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
     for (int t = 0; t < NSM; ++t) {
-      als[t] = 0.f; uus[t] = 0.f; raws[t] = 0.f;
+      als[t] = 0.f; uus[t] = 0.f;
       if (NSC > 0 || t < NS) {
         const int j = W + 1 + t;
-        f32x4_t as = zero4(), au = zero4();
+        // q.k and dOut.v on the VALU: each lane dots its 16-byte chunk, the row's lanes sum
+        // (DPP), and one lane per row hands the pair to the diagonal lane through LDS.  The key
+        // rows are staged (natural row order) for the transposing reads of X and Y.
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          as = mfma_16x16x32(as_bf16x8(kS[t % PF][s]), qB[s], as);
-          au = mfma_16x16x32(as_bf16x8(vS[t % PF][s]), oB[s], au);
+        for (int u = 0; u < CHW; ++u) {
+          const float dk = group_sum<CPR>(dot8_bf16(qR[u], kS[t % PF][u], 0.f));
+          const float dv = group_sum<CPR>(dot8_bf16(oR[u], vS[t % PF][u], 0.f));
+          st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
+          if (rc_chunk<D>(l, u) == 0) sPair[w][rc_row<D>(l, u)] = float2{dk, dv};
         }
-        // Stage the key rows (A layout: row i, chunks 8g + 32s) for the transposing reads.
-#pragma unroll
-        for (int s = 0; s < KS; ++s) st16(sKsw + i * RV + 8 * g + 32 * s, kS[t % PF][s]);
         if (t + PF < NS) {
           const int m0 = n0w - p.taps.delta[W + 1 + t + PF];
 #pragma unroll
-          for (int s = 0; s < KS; ++s) {
-            kS[t % PF][s] = bload16(rK, m0 * ksn + klane + 32 * s);
-            vS[t % PF][s] = bload16(rV, m0 * vsn + vlane + 32 * s);
+          for (int u = 0; u < CHW; ++u) {
+            kS[t % PF][u] = bload16(rK, m0 * ksn + klaneR[u]);
+            vS[t % PF][u] = bload16(rV, m0 * vsn + vlaneR[u]);
           }
         }
-        const float raw = pick4(as, i & 3), uval = pick4(au, i & 3);
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and pairs are written
+        __builtin_amdgcn_wave_barrier();
+        const float2 pr = sPair[w][i];
+        const float raw = pr.x, uval = pr.y;
         const bool ok = diag && row_ok && n >= p.taps.delta[j];
         const float s2 = fmaf(sGain2[j], raw, HAS_SE ? sTw[i * TS + j] : sBias2[j]);
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         als[t] = alpha;
         uus[t] = uval;
-        raws[t] = raw;
+        if (diag) sRAWw[i * TS + j] = c * raw;
         dlane = fmaf(alpha, uval, dlane);
         const float gal = sGain[j] * alpha;
         const s16x4_t b1 = onehot_bf16x4(gal * (uval - D0), i & 3);
         const s16x4_t b2 = onehot_bf16x4(gal, i & 3);
-        __builtin_amdgcn_s_waitcnt(0xc07f);
-        __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const s16x4_t at = lds_read_tr16(ksr + 16 * db);
@@ -299,7 +320,6 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
         if ((unsigned)dl <= (unsigned)W) {
           const float dS = a * al[4 * kk + r] * (uu[4 * kk + r] - Dp);
           sDSw[i * TS + dl] = dS;
-          sRAWw[i * TS + dl] = c * accS[kk][r];
         }
       }
     if (diag) {
@@ -307,7 +327,6 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
       for (int t = 0; t < NSM; ++t)
         if (NSC > 0 || t < NS) {
           sDSw[i * TS + W + 1 + t] = a * als[t] * (uus[t] - Dp);
-          sRAWw[i * TS + W + 1 + t] = c * raws[t];
         }
     }
     if (g == 0) sDp[w * 16 + i] = row_ok ? Dp : 0.f;
