@@ -10,9 +10,11 @@
 //    result layout lane l holds key column l%16 and query rows 4*(l/16)+r, which is exactly the
 //    B operand of dK^T = Q^T (c g dS) and dV^T = dOut^T (a alpha); Q^T and dOut^T come from the
 //    query window [m0, m0+96) in LDS through ds_read_tr16_b64.
-//  * Long-range taps: query rows m0w + delta + 0..15 as the A operand; the wanted values sit on
-//    the diagonal (lane 16*(i/4)+i, register i%4).  Those query / dOut rows are staged in a
-//    wave-private LDS block for the transposed reads of the diagonal update.
+//  * Long-range taps: query rows m0w + delta + 0..15, loaded whole-row (D/8 lanes per row: the
+//    vector L1 serves that at close to four times the rate of the MFMA operand order); q.k,
+//    dOut.v and q.se_j are VALU dot products (v_dot2_f32_bf16, DPP sums over the row's lanes)
+//    handed to the diagonal lane (16*(i/4)+i, register i%4) through LDS.  The query / dOut rows
+//    are staged in a wave-private LDS block for the transposed reads of the diagonal update.
 //  * The q.se_j term of the score (scale_embed) is a [query][tap] table per wave computed on the
 //    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps.
 // Follows _bwd_dkdv_v3 (kernels/dsqg_attention_v3.py:282-352).
@@ -31,6 +33,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
   constexpr int WIN = KT + kMaxWindow;    // query window rows [m0, m0+96)
   constexpr int CPR = D / 8;
   constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
+  constexpr int CHW = D / 32;             // 16-byte chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;
   constexpr int TS = 52;                  // [query][tap] table row stride
@@ -46,6 +49,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain2[kMaxTaps];                 // gain * c * log2e
   __shared__ float sGainC[kMaxTaps];                 // gain * c
+  __shared__ float4 sTrip[4][16];                    // per wave: long-range (q.k, dOut.v, T) of one tap
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -70,8 +74,16 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
   const int m0w = m0 + 16 * w;
   const int m = m0w + i;                  // key row of this lane's MFMA column
   const bool key_ok = m < N;
-  const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
   const int klane = opaque(i * ksn + 8 * g), vlane = opaque(i * vsn + 8 * g);
+  // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
+  int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    qlaneR[u] = opaque(rc_row<D>(l, u) * qsn + rc_chunk<D>(l, u) * 8);
+    olaneR[u] = opaque(rc_row<D>(l, u) * dosn + rc_chunk<D>(l, u) * 8);
+    klaneR[u] = opaque(rc_row<D>(l, u) * ksn + rc_chunk<D>(l, u) * 8);
+    vlaneR[u] = opaque(rc_row<D>(l, u) * vsn + rc_chunk<D>(l, u) * 8);
+  }
 
   // ---- Loads. ----
   uint4 wq[CWIN], wo[CWIN];
@@ -86,6 +98,12 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
   for (int s = 0; s < KS; ++s) {
     kB[s] = as_bf16x8(bload16(rK, m0w * ksn + klane + 32 * s));
     vB[s] = as_bf16x8(bload16(rV, m0w * vsn + vlane + 32 * s));
+  }
+  uint4 kR[CHW], vR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    kR[u] = bload16(rK, m0w * ksn + klaneR[u]);
+    vR[u] = bload16(rV, m0w * vsn + vlaneR[u]);
   }
   // lse (log2 units) and D' of the band's queries m0w + 16qb + 4g + r.
   float lq[12], dq_[12];
@@ -108,15 +126,16 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
       dpS[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
     }
   }
-  uint4 qS[PF][KS], oS[PF][KS];
+  // Long-range query / dOut rows m0w + delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
+  uint4 qS[PF][CHW], oS[PF][CHW];
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
     if (t < NS) {
       const int n0 = m0w + p.taps.delta[W + 1 + t];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        qS[t][s] = bload16(rQ, n0 * qsn + qlane + 32 * s);
-        oS[t][s] = bload16(rO, n0 * dosn + olane + 32 * s);
+      for (int u = 0; u < CHW; ++u) {
+        qS[t][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
+        oS[t][u] = bload16(rO, n0 * dosn + olaneR[u]);
       }
     }
   }
@@ -222,49 +241,41 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
       const int dl = p.taps.delta[j];
-      f32x4_t as = zero4(), au = zero4();
+      // q.k, dOut.v (and q.se_j) on the VALU: each lane dots its 16-byte chunk, the row's lanes
+      // sum (DPP), and one lane per row hands the results to the diagonal lane through LDS.
+      // The query / dOut rows are staged (natural row order) for the transposing reads.
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        as = mfma_16x16x32(as_bf16x8(qS[t % PF][s]), kB[s], as);
-        au = mfma_16x16x32(as_bf16x8(oS[t % PF][s]), vB[s], au);
-      }
-      float tq;  // log2e (bias + c q.se) for query row i of this block
-      if constexpr (HAS_SE) {
-        float part = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const bf16x8_t qv = as_bf16x8(qS[t % PF][s]);
-          const bf16x8_t sv = *reinterpret_cast<const bf16x8_t*>(sSE + j * RV + 32 * s + 8 * g);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) part = fmaf((float)qv[e], (float)sv[e], part);
+      for (int u = 0; u < CHW; ++u) {
+        const float dk = group_sum<CPR>(dot8_bf16(qS[t % PF][u], kR[u], 0.f));
+        const float dv = group_sum<CPR>(dot8_bf16(oS[t % PF][u], vR[u], 0.f));
+        float tqr = sBias2[j];  // log2e (bias + c q.se) for this query row
+        if constexpr (HAS_SE) {
+          const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
+          tqr = fmaf(c2, group_sum<CPR>(dot8_bf16(qS[t % PF][u], se, 0.f)), tqr);
         }
-        tq = fmaf(c2, col_sum(part), sBias2[j]);
-      } else {
-        tq = sBias2[j];
-      }
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        st16(qsw + i * RV + 8 * g + 32 * s, qS[t % PF][s]);
-        st16(osw + i * RV + 8 * g + 32 * s, oS[t % PF][s]);
+        st16(qsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qS[t % PF][u]);
+        st16(osw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, oS[t % PF][u]);
+        if (rc_chunk<D>(l, u) == 0) sTrip[w][rc_row<D>(l, u)] = float4{dk, dv, tqr, 0.f};
       }
       if (t + PF < NS) {
         const int n0 = m0w + p.taps.delta[W + 1 + t + PF];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          qS[t % PF][s] = bload16(rQ, n0 * qsn + qlane + 32 * s);
-          oS[t % PF][s] = bload16(rO, n0 * dosn + olane + 32 * s);
+        for (int u = 0; u < CHW; ++u) {
+          qS[t % PF][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
+          oS[t % PF][u] = bload16(rO, n0 * dosn + olaneR[u]);
         }
       }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and results are written
+      __builtin_amdgcn_wave_barrier();
+      const float4 tr = sTrip[w][i];
       const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
       const float lseq = lseS[t], dpq = dpS[t];
       const bool ok = diag && key_ok && nq < N;
-      const float raw = pick4(as, i & 3), uval = pick4(au, i & 3);
+      const float raw = tr.x, uval = tr.y, tq = tr.z;
       const float alpha = ok ? __builtin_amdgcn_exp2f(fmaf(sGain2[j], raw, tq) - lseq) : 0.f;
       const float dS = a * alpha * (uval - dpq);
       const s16x4_t bk = onehot_bf16x4(sGainC[j] * dS, i & 3);
       const s16x4_t bv = onehot_bf16x4(a * alpha, i & 3);
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         dK[db] = mfma_16x16x16(lds_read_tr16(qtr + 16 * db), bk, dK[db]);
