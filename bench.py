@@ -36,12 +36,15 @@ def _events_ms(fn, reps, stream):
     return start.elapsed_time(end) / reps
 
 
-def cpu_baseline(w, inp_cpu):
-    """CPU oracle (fp32 autograd restatement of the reference) on one sequence of the workload."""
+def cpu_baseline(w, inp_cpu, min_seconds=10.0, max_reps=20):
+    """CPU oracle (fp32 autograd restatement of the reference) on the whole workload batch.
+
+    One warm-up call, then whole-batch fwd+bwd calls until at least `min_seconds` of CPU work
+    (and at least 3 calls) have been timed; value = tokens processed / time.
+    """
     import torch
     from oracle import dsqg_forward_backward
-    b = 0
-    sl = {k: (v[b:b + 1].float() if k in ("q", "k", "v", "dout") else v) for k, v in inp_cpu.items()}
+    sl = {k: (v.float() if k in ("q", "k", "v", "dout") else v) for k, v in inp_cpu.items()}
     threads = torch.get_num_threads()
 
     def run():
@@ -51,16 +54,18 @@ def cpu_baseline(w, inp_cpu):
 
     run()  # warm-up
     times = []
-    for _ in range(3):
+    while len(times) < max_reps and (len(times) < 3 or sum(times) < min_seconds):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": round(w.N / t, 1), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"1 of {w.B} sequences of config {w.index} (H{w.H} N{w.N} D{w.D} "
-                       f"J{w.J}), fwd+bwd, oracle/dsqg_oracle.py fp32 autograd, median of 3 "
-                       f"after 1 warm-up, torch threads={threads}"),
-            "seconds_per_sequence": round(t, 3)}
+        print(f"[bench] cpu oracle call {len(times)}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
+    total = sum(times)
+    tokens = w.B * w.N * len(times)
+    return {"value": round(tokens / total, 1), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"whole config-{w.index} batch (B{w.B} H{w.H} N{w.N} D{w.D} J{w.J}) fwd+bwd, "
+                       f"oracle/dsqg_oracle.py fp32 autograd, {len(times)} calls after 1 warm-up, "
+                       f"{total:.1f} s timed, torch threads={threads}"),
+            "seconds_per_call": round(total / len(times), 3)}
 
 
 def bench_decode(dev, steps=1000):
