@@ -111,6 +111,60 @@ def bench_decode(dev, steps=1000):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "timing": "hipGraph replay, HIP events"}
 
 
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "hbm_traffic_config2.md")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or None.
+
+    The summary holds lines `traffic_bytes_per_launch <kernel> = <bytes>`: FETCH_SIZE plus
+    WRITE_SIZE of the kernel (two rocprofv3 --pmc passes of `bench.py --profile-kernel`), each
+    scaled by what the same counter reads for a plain device copy of known size.
+    """
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                parts = line.replace("`", "").split()
+                if len(parts) == 4 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                    return int(parts[3])
+    except OSError:
+        pass
+    return None
+
+
+def profile_mode(args, w, dev):
+    """Launches one kernel of the workload a few times and a plain copy of known size."""
+    import torch
+    from dwarf_amd import ops
+    from dwarf_amd.workloads import make_inputs
+    inp = make_inputs(w, device="cpu", seed=w.seed)
+    d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+    fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
+                       d["score_gain"], d["if_gain"], list(w.offsets))
+    bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
+                       d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
+                       d["scale_embed"] is not None, d["score_gain"] is not None,
+                       d["if_gain"] is not None)
+    fl.run()
+    bl.run()
+    torch.cuda.synchronize()
+    for _ in range(args.profile_reps):
+        if args.profile_kernel == "fwd":
+            fl.run()
+        else:
+            bl.run(args.profile_kernel)
+    nbytes = args.copy_mib << 20
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.profile_reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] profile mode: {args.profile_reps} launches of {args.profile_kernel}, "
+          f"{args.profile_reps} copies of {nbytes} bytes", file=sys.stderr, flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +175,12 @@ def main(argv=None):
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv"], default=None,
+                    help="counter-collection mode: launch only this kernel --profile-reps times, "
+                         "plus a plain device copy of --copy-mib MiB (the scale reference for "
+                         "FETCH_SIZE / WRITE_SIZE), then exit without a JSON line")
+    ap.add_argument("--profile-reps", type=int, default=5)
+    ap.add_argument("--copy-mib", type=int, default=256)
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -143,6 +203,9 @@ def main(argv=None):
     E = 2
     print(f"[bench] config {w.index}: B{w.B} H{w.H} N{w.N} D{w.D} J{w.J} {w.dtype}, "
           f"{args.sets} input sets, warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
+
+    if args.profile_kernel:
+        return profile_mode(args, w, dev)
 
     sets = []
     for i in range(args.sets):
@@ -190,8 +253,9 @@ def main(argv=None):
     dom = max((k for k in per if "algorithmic_bytes" in per[k]), key=lambda k: per[k]["us"])
     achieved = per[dom]["achieved_GBs"]
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
-                "launch_us": per[dom]["us"], "algorithmic_bytes": per[dom]["algorithmic_bytes"]}
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
+                "kernel": dom, "launch_us": per[dom]["us"],
+                "algorithmic_bytes": per[dom]["algorithmic_bytes"]}
 
     step_bytes = w.fwd_bytes() + w.bwd_bytes()
     tok_s = w.B * w.N / (ms * 1e-3)
