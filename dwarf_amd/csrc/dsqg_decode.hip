@@ -8,7 +8,8 @@
 //
 // One wave64 per (b,h), four per workgroup.  Lanes form R = 64/G groups of G = D/8 lanes; in
 // pass t group r handles tap j = t*R + r, so the J key and value rows are fetched as R
-// coalesced rows at a time, all of them requested before any arithmetic.  The softmax max/sum
+// coalesced rows at a time, all of them requested before any arithmetic (two dependent memory
+// round trips per step: the position, then the ring rows it selects).  The softmax max/sum
 // and the output sum across groups use DPP and v_permlane16/32_swap (no LDS).
 //
 // The reference has no decode kernel (train/train_2048_condU.py:463-487 recomputes the prefix);
@@ -77,39 +78,67 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
   T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
 
-  // Every K and V row of this lane group's taps is requested before any arithmetic: one memory
-  // round trip per step.  Masked taps (pos - delta < 0) read a valid slot and are zeroed.
-  float q[8];
-  Vec8<T>::load(qrow + d0, q);
-  float kx[P][8], vx[P][8];
+  // Two memory round trips per step: everything that does not depend on the position (query,
+  // new key/value row, per-tap bias and gain) goes out together with the position itself; the
+  // ring rows of the taps follow, all requested before any arithmetic.  Tap 0 (delta = 0) is
+  // the new row, already in registers; so is the row written into the ring at the end.
+  constexpr int C16 = sizeof(T) == 4 ? 2 : 1;  // 16-byte chunks per lane (8 elements)
+  uint4 qraw[C16], knraw[C16], vnraw[C16];
+#pragma unroll
+  for (int u = 0; u < C16; ++u) {
+    qraw[u] = ld16(qrow + d0 + 4 * u * (sizeof(T) == 4));
+    knraw[u] = ld16(knew + d0 + 4 * u * (sizeof(T) == 4));
+    vnraw[u] = ld16(vnew + d0 + 4 * u * (sizeof(T) == 4));
+  }
+  float pbias[P], pgain[P];
+#pragma unroll
+  for (int t = 0; t < P; ++t) {
+    const int j = t * R + r;
+    const int jj = j < J ? j : 0;
+    pbias[t] = p.pos_bias[jj * p.H + h];
+    pgain[t] = p.score_gain ? p.score_gain[h * J + jj] : 1.0f;
+  }
+
+  // Masked taps (pos - delta < 0) read a valid slot and are zeroed.
+  uint4 kraw[P][C16], vraw[P][C16];
   bool ok[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const int j = t * R + r;
     const int dl = j < J ? p.taps.delta[j] : 0;
     ok[t] = j < J && pos - dl >= 0;
-    const long long sl = ok[t] ? (pos - dl) % S : 0;
-    const T* ks = dl == 0 ? knew : kring + sl * D;
-    const T* vs = dl == 0 ? vnew : vring + sl * D;
-    Vec8<T>::load(ks + d0, kx[t]);
-    Vec8<T>::load(vs + d0, vx[t]);
+    if (dl > 0) {
+      const long long sl = ok[t] ? (pos - dl) % S : 0;
+#pragma unroll
+      for (int u = 0; u < C16; ++u) {
+        kraw[t][u] = ld16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4));
+        vraw[t][u] = ld16(vring + sl * D + d0 + 4 * u * (sizeof(T) == 4));
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < C16; ++u) { kraw[t][u] = knraw[u]; vraw[t][u] = vnraw[u]; }
+    }
   }
 
+  float q[8];
+  Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
   float s[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const int j = t * R + r;
     const int jj = j < J ? j : 0;
+    float kx[8];
+    Vec8<T>::load(reinterpret_cast<const T*>(kraw[t]), kx);
     float pk = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[t][e], pk);
-    float part = pk * (p.score_gain ? p.score_gain[h * J + jj] : 1.0f);
+    for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[e], pk);
+    float part = pk * pgain[t];
     if constexpr (HAS_SE) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[jj * D + d0 + e], part);
     }
     const float tot = group_sum<G>(part);
-    s[t] = ok[t] ? fmaf(tot, c, p.pos_bias[jj * p.H + h]) : -INFINITY;
+    s[t] = ok[t] ? fmaf(tot, c, pbias[t]) : -INFINITY;
   }
 
   float mx = -INFINITY;
@@ -124,8 +153,10 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   for (int t = 0; t < P; ++t) {
     const float pj = __expf(s[t] - mx);
     l += pj;
+    float vx[8];
+    Vec8<T>::load(reinterpret_cast<const T*>(vraw[t]), vx);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, ok[t] ? vx[t][e] : 0.f, acc[e]);
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, ok[t] ? vx[e] : 0.f, acc[e]);
   }
   l = groups_reduce_sum<R>(l);
 #pragma unroll
@@ -140,10 +171,11 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     Vec8<T>::store(outrow + d0, o);
     // The new row goes into slot pos mod S (read by later steps only).
     const long long sl = pos % S;
-    st16(kring + sl * D + d0, ld16(knew + d0));
-    if constexpr (sizeof(T) == 4) st16(kring + sl * D + d0 + 4, ld16(knew + d0 + 4));
-    st16(vring + sl * D + d0, ld16(vnew + d0));
-    if constexpr (sizeof(T) == 4) st16(vring + sl * D + d0 + 4, ld16(vnew + d0 + 4));
+#pragma unroll
+    for (int u = 0; u < C16; ++u) {
+      st16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4), knraw[u]);
+      st16(vring + sl * D + d0 + 4 * u * (sizeof(T) == 4), vnraw[u]);
+    }
     if (p.pos_next && h == 0 && g == 0) p.pos_next[b] = pos + 1;
   }
 }
