@@ -99,7 +99,9 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     pgain[t] = p.score_gain ? p.score_gain[h * J + jj] : 1.0f;
   }
 
-  // Masked taps (pos - delta < 0) read a valid slot and are zeroed.
+  // Masked taps (pos - delta < 0) read a valid slot and are zeroed.  Slot of tap delta:
+  // (pos mod S) - delta, wrapped once (0 < delta < S).
+  const int base = (int)(pos % S);
   uint4 kraw[P][C16], vraw[P][C16];
   bool ok[P];
 #pragma unroll
@@ -108,7 +110,8 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     const int dl = j < J ? p.taps.delta[j] : 0;
     ok[t] = j < J && pos - dl >= 0;
     if (dl > 0) {
-      const long long sl = ok[t] ? (pos - dl) % S : 0;
+      const int sw = base - dl;
+      const long long sl = ok[t] ? (sw < 0 ? sw + S : sw) : 0;
 #pragma unroll
       for (int u = 0; u < C16; ++u) {
         kraw[t][u] = ld16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4));
@@ -170,7 +173,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     for (int e = 0; e < 8; ++e) o[e] = acc[e] * inv;
     Vec8<T>::store(outrow + d0, o);
     // The new row goes into slot pos mod S (read by later steps only).
-    const long long sl = pos % S;
+    const long long sl = base;
 #pragma unroll
     for (int u = 0; u < C16; ++u) {
       st16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4), knraw[u]);
