@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
 
   // Masked taps (pos - delta < 0) read a valid slot and are zeroed.  Slot of tap delta:
   // (pos mod S) - delta, wrapped once (0 < delta < S).
-  const int base = (int)(pos % S);
+  const int base = (pos >> 31) == 0 ? (int)pos % S : (int)(pos % S);  // 32-bit when it fits
   uint4 kraw[P][C16], vraw[P][C16];
   bool ok[P];
 #pragma unroll
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     ok[t] = j < J && pos - dl >= 0;
     if (dl > 0) {
       const int sw = base - dl;
-      const long long sl = ok[t] ? (sw < 0 ? sw + S : sw) : 0;
+      const int sl = ok[t] ? (sw < 0 ? sw + S : sw) : 0;
 #pragma unroll
       for (int u = 0; u < C16; ++u) {
         kraw[t][u] = ld16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4));
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     for (int e = 0; e < 8; ++e) o[e] = acc[e] * inv;
     Vec8<T>::store(outrow + d0, o);
     // The new row goes into slot pos mod S (read by later steps only).
-    const long long sl = base;
+    const int sl = base;
 #pragma unroll
     for (int u = 0; u < C16; ++u) {
       st16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4), knraw[u]);
