@@ -1,0 +1,150 @@
+"""Drop-in attention modules: the reference's parameter names, shapes and initialisation, with
+the DSQG core on the HIP kernels.
+
+State dicts saved from the reference modules load unchanged (``load_state_dict(strict=True)``):
+
+* ``DSQGAttentionV3``      -- kernels/dsqg_attention_v3.py:463-536 (pos_bias, scale_embed)
+* ``DSQGAttentionQW``      -- train/train_2048_condU.py:116-205 (adds if_gain) and, with the
+  47-offset table, train/train_4096_13m_condU.py:110-175
+* ``DSQGAttentionN_Fused`` -- kernels/dsqg_attention_v2.py:434-471 (pos_bias only, gate bias 2)
+
+Forward semantics follow the reference modules: qkv projection, optional Huygens K/V injection
+(``kv_inject=(k_delta, v_delta)`` added to K and V only), DSQG attention, per-head IF gain
+(QW), ``out_proj(out * sigmoid(gate_proj(x)))`` and dropout.  Differences that change no
+result beyond rounding:
+
+* q, k, v go to the kernels as strided [B,H,N,HD] views of the projection output [B,N,3D]
+  (the kernels take row strides), so the three ``permute(...).contiguous()`` copies of the
+  reference are gone;
+* the IF gain is applied inside the forward kernel (fp32, before the bf16 rounding of the
+  output) and its gradient comes from the backward kernel.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+from torch import Tensor, nn
+
+from .api import dsqg_attention
+from .offsets import OFFSETS_V3, validate
+
+
+def _log_linear_bias(offsets: Sequence[int], num_heads: int) -> Tensor:
+    """pos_bias[j,h] = -log(1 + delta_j) * linspace(0.2, 2.0, H)[h] (the reference's init)."""
+    alphas = torch.linspace(0.2, 2.0, num_heads)
+    delta_vals = torch.tensor([math.log(1.0 + d) for d in offsets], dtype=torch.float32)
+    return -delta_vals.unsqueeze(1) * alphas.unsqueeze(0)
+
+
+def _heads(qkv: Tensor, B: int, N: int, H: int, HD: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """q, k, v as [B,H,N,HD] views of qkv [B,N,3*H*HD] (row stride 3*H*HD, no copy)."""
+    q, k, v = qkv.split(H * HD, dim=-1)
+    return tuple(t.view(B, N, H, HD).permute(0, 2, 1, 3) for t in (q, k, v))
+
+
+class _DSQGBase(nn.Module):
+    def __init__(self, embedding_dim: int, num_heads: int, offsets: Sequence[int],
+                 dropout: float, gate_bias: float):
+        super().__init__()
+        assert embedding_dim % num_heads == 0, "embedding_dim must be a multiple of num_heads"
+        self.embedding_dim = embedding_dim
+        self.num_heads = num_heads
+        self.head_dim = embedding_dim // num_heads
+        self._offsets = list(offsets)
+        self.qkv_proj = nn.Linear(embedding_dim, 3 * embedding_dim, bias=True)
+        self.out_proj = nn.Linear(embedding_dim, embedding_dim, bias=True)
+        self.gate_proj = nn.Linear(embedding_dim, embedding_dim, bias=True)
+        nn.init.constant_(self.gate_proj.bias, gate_bias)
+        self.pos_bias = nn.Parameter(_log_linear_bias(self._offsets, num_heads))
+        self.dropout = nn.Dropout(dropout)
+
+    def _attend(self, x: Tensor, kv_inject, scale_embed: Optional[Tensor],
+                if_gain: Optional[Tensor]) -> Tensor:
+        B, N, D = x.shape
+        H, HD = self.num_heads, self.head_dim
+        q, k, v = _heads(self.qkv_proj(x), B, N, H, HD)
+        if kv_inject is not None:
+            k_delta, v_delta = kv_inject
+            k = k + k_delta
+            v = v + v_delta
+        out = dsqg_attention(q, k, v, self.pos_bias, scale_embed, offsets=self._offsets,
+                             if_gain=if_gain)
+        out_flat = out.permute(0, 2, 1, 3).reshape(B, N, D)
+        gate = torch.sigmoid(self.gate_proj(x))
+        return self.dropout(self.out_proj(out_flat * gate))
+
+    def _summary(self) -> dict:
+        with torch.no_grad():
+            pb = self.pos_bias.detach().cpu()
+        return {"pos_bias_abs_mean": pb.abs().mean().item(),
+                "pos_bias_abs_max": pb.abs().max().item(),
+                "pos_bias_mean_per_head": pb.mean(0).tolist()}
+
+
+class DSQGAttentionV3(_DSQGBase):
+    """kernels/dsqg_attention_v3.py:463-536: pos_bias [J,H], scale_embed [J,HD] (zero init),
+    gate bias 0; registers the offset table as the buffer ``offsets``."""
+
+    def __init__(self, embedding_dim: int, num_heads: int, seq_len: int = 2048,
+                 offsets: Optional[Sequence[int]] = None, dropout: float = 0.1):
+        offs = validate(offsets) if offsets is not None else list(OFFSETS_V3)
+        super().__init__(embedding_dim, num_heads, offs, dropout, gate_bias=0.0)
+        self.register_buffer("offsets", torch.tensor(offs, dtype=torch.long))
+        self.n_offsets = len(offs)
+        self.scale_embed = nn.Parameter(torch.zeros(len(offs), self.head_dim))
+
+    def forward(self, x: Tensor, kv_inject=None) -> Tensor:
+        return self._attend(x, kv_inject, self.scale_embed, None)
+
+    def attn_summary(self) -> dict:
+        s = self._summary()
+        with torch.no_grad():
+            se = self.scale_embed.detach().cpu()
+        s.update(scale_embed_abs_mean=se.abs().mean().item(), scale_embed_abs_max=se.abs().max().item())
+        return s
+
+
+class DSQGAttentionQW(_DSQGBase):
+    """train/train_2048_condU.py:116-205: pos_bias [J,H], scale_embed [J,HD] (zero init),
+    if_gain [H] (one init), gate bias 0.  ``offsets`` defaults to the 44-offset table; the
+    47-offset table gives the N=4096 trainer's module (train/train_4096_13m_condU.py:110)."""
+
+    def __init__(self, embedding_dim: int, num_heads: int, seq_len: int = 2048,
+                 dropout: float = 0.1, offsets: Optional[Sequence[int]] = None):
+        offs = validate(offsets) if offsets is not None else list(OFFSETS_V3)
+        super().__init__(embedding_dim, num_heads, offs, dropout, gate_bias=0.0)
+        self.scale_embed = nn.Parameter(torch.zeros(len(offs), self.head_dim))
+        self.if_gain = nn.Parameter(torch.ones(num_heads))
+
+    def forward(self, x: Tensor, kv_inject=None) -> Tensor:
+        return self._attend(x, kv_inject, self.scale_embed, self.if_gain)
+
+    def attn_summary(self) -> dict:
+        s = self._summary()
+        with torch.no_grad():
+            se = self.scale_embed.detach().cpu()
+            gain = self.if_gain.detach().cpu()
+        s.update(scale_embed_abs_mean=se.abs().mean().item(), scale_embed_abs_max=se.abs().max().item(),
+                 if_gain=gain.tolist())
+        return s
+
+
+class DSQGAttentionN_Fused(_DSQGBase):
+    """kernels/dsqg_attention_v2.py:434-471: pos_bias [J,H] only, gate bias 2; registers the
+    offset table as the buffer ``offsets``."""
+
+    def __init__(self, embedding_dim: int, num_heads: int, seq_len: int = 2048,
+                 offsets: Optional[Sequence[int]] = None, dropout: float = 0.1):
+        offs = validate(offsets) if offsets is not None else list(OFFSETS_V3)
+        super().__init__(embedding_dim, num_heads, offs, dropout, gate_bias=2.0)
+        self.register_buffer("offsets", torch.tensor(offs, dtype=torch.long))
+        self.n_offsets = len(offs)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self._attend(x, None, None, None)
+
+    def attn_summary(self) -> dict:
+        return self._summary()
