@@ -8,7 +8,8 @@ input sets are rotated so that consecutive steps cannot be served from the 256 M
 Prints one JSON line: tok/s (B*N per step), the roofline of the dominant kernel (algorithmic
 bytes per launch over its average launch time, HIP events on the launch stream), the
 fraction of HBM peak for the whole fwd+bwd step, the ring-buffer decode step (workload 4,
-1000 steps replayed from a HIP graph), and the CPU oracle timed on a bounded sample.
+1000 steps replayed from a HIP graph), the drop-in DSQGAttentionQW layer fwd+bwd, and the CPU
+oracle timed on a bounded sample.
 """
 
 from __future__ import annotations
@@ -111,6 +112,39 @@ def bench_decode(dev, steps=1000):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "timing": "hipGraph replay, HIP events"}
 
 
+def bench_module(dev, steps=20, warmup=5):
+    """DSQGAttentionQW (E768 H12, the config-2 attention layer) fwd+bwd in bf16 on x [8,2048,768]:
+    as shipped (q, k, v strided views of the qkv projection) and with the reference's
+    permute().contiguous() copies put back (train/train_2048_condU.py:173-175)."""
+    import torch
+    from dwarf_amd import dsqg_attention
+    from dwarf_amd.modules import DSQGAttentionQW, _heads
+    B, N, E, H = 8, 2048, 768, 12
+    torch.manual_seed(3)
+    m = DSQGAttentionQW(E, H, dropout=0.0).to(dev, torch.bfloat16)
+    x = torch.randn(B, N, E, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    dy = torch.randn(B, N, E, device=dev, dtype=torch.bfloat16)
+
+    def contiguous_copy_forward(x):
+        q, k, v = (t.contiguous() for t in _heads(m.qkv_proj(x), B, N, H, E // H))
+        out = dsqg_attention(q, k, v, m.pos_bias, m.scale_embed, if_gain=m.if_gain)
+        flat = out.permute(0, 2, 1, 3).reshape(B, N, E)
+        return m.out_proj(flat * torch.sigmoid(m.gate_proj(x)))
+
+    res = {"workload": "DSQGAttentionQW E768 H12, x [8,2048,768] bf16, fwd+bwd incl. projections",
+           "steps": steps}
+    stream = torch.cuda.current_stream(dev)
+    for name, fwd in (("strided_views", m), ("contiguous_copies", contiguous_copy_forward)):
+        def step(i):
+            fwd(x).backward(dy)
+        for i in range(warmup):
+            step(i)
+        ms = _events_ms(step, steps, stream)
+        res[f"ms_per_step_{name}"] = round(ms, 4)
+    res["tok_per_s"] = round(B * N / (res["ms_per_step_strided_views"] * 1e-3), 1)
+    return res
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "hbm_traffic_config2.md")
 
@@ -175,6 +209,7 @@ def main(argv=None):
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
     ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv"], default=None,
                     help="counter-collection mode: launch only this kernel --profile-reps times, "
                          "plus a plain device copy of --copy-mib MiB (the scale reference for "
@@ -275,6 +310,11 @@ def main(argv=None):
     if not args.no_decode:
         result["decode"] = bench_decode(dev, args.decode_steps)
         print(f"[bench] decode {result['decode']['us_per_step']} us/step", file=sys.stderr, flush=True)
+    if not args.no_module:
+        result["module"] = bench_module(dev)
+        print(f"[bench] module QW fwd+bwd {result['module']['ms_per_step_strided_views']} ms "
+              f"(with permute copies {result['module']['ms_per_step_contiguous_copies']} ms)",
+              file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, sets[0][0])
