@@ -18,10 +18,10 @@
 //  5. Softmax over each query's J taps in registers: the four lanes of a query column combine
 //     max and sum with two cross-lane steps; lse = max + log(sum); the weights are normalised
 //     (and scaled by the IF gain) before P V.
-//  6. P V: O^T = V^T P^T with v_mfma_f32_16x16x16_bf16.  V^T comes from the row-major LDS tile
-//     through ds_read_tr16_b64; P^T is already in B layout.  Long-range taps stage their V
-//     rows [n0-delta, n0-delta+64) in a double-buffered LDS block and multiply by a diagonal
-//     P^T that is non-zero in one register of the diagonal lane only.
+//  6. Dense P V: O^T = V^T P^T with v_mfma_f32_16x16x16_bf16.  V^T comes from the row-major LDS
+//     tile through ds_read_tr16_b64; P^T is already in B layout.  Long-range P V on the VALU in
+//     the whole-row layout (each lane adds p * v for its rows' 16-byte chunk, the weights read
+//     from the wave's table); the two parts meet in LDS and leave as 16-byte row stores.
 //
 // Semantics: _fwd_v3, kernels/dsqg_attention_v3.py:60-163 (plus score gain and IF gain).
 #include "dsqg_common.hpp"
@@ -272,36 +272,74 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
     for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vr + 16 * db), pb, accO[db]);
   }
 
-  // ---- Long-range P V through the wave-private LDS block: O^T += V_t^T diag(p_t). ----
-  bf16_t* buf = sVs[w];
-  const bf16_t* vr = buf + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+  // ---- Long-range P V on the VALU, whole-row layout: o_L[row] += p_t[row] * v_t[row]. ----
+  // The diagonal lanes publish the normalised long-range weights in the wave's table; every
+  // lane then adds p * v for the 16-byte chunk of its rows, with no per-tap LDS round trip.
+  if (diag) {
+#pragma unroll
+    for (int t = 0; t < NSM; ++t)
+      if (NSC > 0 || t < NS) sRw[i * 16 + t] = ss[t] * inv;
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the weights are in the table
+  __builtin_amdgcn_wave_barrier();
+  float oL[CHW][8];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) oL[u][e] = 0.f;
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
 #pragma unroll
       for (int u = 0; u < CHW; ++u) {
-        const int ci = l + 64 * u;
-        st16(buf + (ci / CPR) * RV + (ci % CPR) * 8, vS[t % PF][u]);
+        const float pw = sRw[rc_row<D>(l, u) * 16 + t];
+        const uint4 x = vS[t % PF][u];
+        const unsigned wd[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          oL[u][2 * e] = fmaf(pw, __uint_as_float(wd[e] << 16), oL[u][2 * e]);
+          oL[u][2 * e + 1] = fmaf(pw, __uint_as_float(wd[e] & 0xffff0000u), oL[u][2 * e + 1]);
+        }
       }
       if (t + PF < NS) {
         const int r0 = n0w - p.taps.delta[W + 1 + t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) vS[t % PF][u] = bload16(rV, r0 * vsn + vlane[u]);
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the block is in LDS
-      __builtin_amdgcn_wave_barrier();
-      const s16x4_t bd = onehot_bf16x4(ss[t] * inv, i & 3);  // zero outside the diagonal lane
-#pragma unroll
-      for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vr + 16 * db), bd, accO[db]);
     }
   }
 
-  if (row_ok) {
-    bf16_t* ob = static_cast<bf16_t*>(p.out) + b * p.os.b + h * p.os.h + n * p.os.n + 4 * g;
+  // ---- out = O_dense (MFMA layout) + o_L (row layout), stored as whole rows. ----
+  // Two rounds of 8 rows through the wave's free staging block (8 x (D+4) floats each): the
+  // MFMA lanes of those rows deposit their values, the row-layout lanes add theirs and store
+  // 16 bytes per lane.
+  float* xb = reinterpret_cast<float*>(sVs[w]);
+  constexpr int XS = D + 4;
+  bf16_t* outb = static_cast<bf16_t*>(p.out) + b * p.os.b + h * p.os.h;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-      *reinterpret_cast<uint2*>(ob + 16 * db) =
-          pack_bf16x4_u2(accO[db][0], accO[db][1], accO[db][2], accO[db][3]);
+  for (int half = 0; half < 2; ++half) {
+    if ((i >> 3) == half) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        *reinterpret_cast<float4*>(xb + (i & 7) * XS + 16 * db + 4 * g) =
+            make_float4(accO[db][0], accO[db][1], accO[db][2], accO[db][3]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < CHW; ++u) {
+      const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+      if ((rr >> 3) == half && n0w + rr < N) {
+        const float* src = xb + (rr & 7) * XS + 8 * cc;
+        const float4 lo = *reinterpret_cast<const float4*>(src);
+        const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+        const uint2 a0 = pack_bf16x4_u2(lo.x + oL[u][0], lo.y + oL[u][1], lo.z + oL[u][2], lo.w + oL[u][3]);
+        const uint2 a1 = pack_bf16x4_u2(hi.x + oL[u][4], hi.y + oL[u][5], hi.z + oL[u][6], hi.w + oL[u][7]);
+        st16(outb + (n0w + rr) * p.os.n + 8 * cc, make_uint4(a0.x, a0.y, a1.x, a1.y));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // this round's reads are done before the next writes
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
