@@ -6,7 +6,7 @@ A step is one DSQG forward + backward over one batch of the headline workload (c
 B8 H12 N2048 D64, bf16, 44 offsets, synthetic seeded inputs already resident in HBM).  Three
 input sets are rotated so that consecutive steps cannot be served from the 256 MB Infinity Cache.
 Prints one JSON line: tok/s (B*N per step), the roofline of the dominant kernel (algorithmic
-bytes per launch over its average launch time, HIP events on the launch stream), the
+bytes per launch over its median launch time, HIP events on the launch stream), the
 fraction of HBM peak for the whole fwd+bwd step, the ring-buffer decode step (workload 4,
 1000 steps replayed from a HIP graph), the drop-in DSQGAttentionQW layer fwd+bwd, and the CPU
 oracle timed on a bounded sample.
@@ -25,16 +25,34 @@ HBM_PEAK_GBS = 8000.0
 
 
 def _events_ms(fn, reps, stream):
+    """Median over `reps` calls of fn(i), each bracketed by its own pair of HIP events on
+    `stream` (events only, no synchronisation between calls)."""
     import torch
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     torch.cuda.synchronize()
-    start.record(stream)
+    ev[0].record(stream)
     for i in range(reps):
         fn(i)
-    end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) / reps
+        ev[i + 1].record(stream)
+    ev[-1].synchronize()
+    return statistics.median(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+
+
+def _cpu_identity():
+    """os.cpu_count(), torch's thread count and the lscpu model name of this host."""
+    import platform
+    import subprocess
+    import torch
+    model = platform.processor() or ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cpu_model": model}
 
 
 def cpu_baseline(w, inp_cpu, min_seconds=10.0, max_reps=20):
@@ -66,7 +84,31 @@ def cpu_baseline(w, inp_cpu, min_seconds=10.0, max_reps=20):
             "sample": (f"whole config-{w.index} batch (B{w.B} H{w.H} N{w.N} D{w.D} J{w.J}) fwd+bwd, "
                        f"oracle/dsqg_oracle.py fp32 autograd, {len(times)} calls after 1 warm-up, "
                        f"{total:.1f} s timed, torch threads={threads}"),
-            "seconds_per_call": round(total / len(times), 3)}
+            "seconds_per_call": round(total / len(times), 3), **_cpu_identity()}
+
+
+def cpu_baseline_decode(steps=10):
+    """CPU oracle decode step (ring restatement, fp32) on the decode workload, `steps` steps."""
+    import torch
+    from oracle import decode_step
+    from dwarf_amd.workloads import DECODE, make_decode_inputs
+    d = make_decode_inputs(device="cpu")
+    f = {k: (v.float() if v.is_floating_point() else v) for k, v in d.items()}
+    pos = f["pos"].clone()
+    decode_step(f["q"], f["k_new"], f["v_new"], f["k_ring"], f["v_ring"], pos, f["pos_bias"],
+                offsets=DECODE["offsets"])  # warm-up
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        pos += 1
+        decode_step(f["q"], f["k_new"], f["v_new"], f["k_ring"], f["v_ring"], pos, f["pos_bias"],
+                    offsets=DECODE["offsets"])
+    dt = (time.perf_counter() - t0) / steps
+    return {"value": round(DECODE["B"] / dt, 1), "unit": "tok/s", "kind": "port",
+            "cores": torch.get_num_threads(),
+            "sample": (f"decode workload (B{DECODE['B']} H{DECODE['H']} D{DECODE['D']} ring "
+                       f"{DECODE['S']}), oracle/dsqg_oracle.py decode_step fp32, {steps} steps "
+                       f"after 1 warm-up"),
+            "ms_per_step": round(dt * 1e3, 3)}
 
 
 def bench_decode(dev, steps=1000):
@@ -318,6 +360,8 @@ def main(argv=None):
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, sets[0][0])
+        if "decode" in result:
+            result["decode"]["cpu_baseline"] = cpu_baseline_decode()
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
