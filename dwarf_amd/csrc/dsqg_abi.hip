@@ -55,8 +55,11 @@ int hip_status(hipError_t e) { return e == hipSuccess ? DSQG_OK : DSQG_EHIP; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct BwdLayout {
-  size_t dpre, part_bias, part_gain, part_if, part_se, total;
+  size_t dpre, part_bias, part_gain, part_if, part_se, se_stage, total;
+  int se_slices, se_per;  // two-stage dscale_embed sum: slices of se_per workgroup partials
 };
+
+constexpr size_t kMaxSeSlices = 64;
 
 BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
   const dsqg_shape& s = a.shape;
@@ -68,6 +71,12 @@ BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
   L.part_gain = off; if (a.dscore_gain) off = align256(off + sizeof(float) * nb * s.J);
   L.part_if = off; if (a.dif_gain) off = align256(off + sizeof(float) * nb);
   L.part_se = off; if (a.dscale_embed) off = align256(off + sizeof(float) * nb * s.J * s.D);
+  L.se_slices = 0; L.se_per = 0;
+  if (nb > 0) {
+    L.se_per = (int)((nb + kMaxSeSlices - 1) / kMaxSeSlices);
+    L.se_slices = (int)((nb + L.se_per - 1) / L.se_per);
+  }
+  L.se_stage = off; if (a.dscale_embed) off = align256(off + sizeof(float) * L.se_slices * s.J * s.D);
   L.total = off;
   return L;
 }
@@ -206,6 +215,9 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
     r.part_gain = p.part_gain; r.part_if = p.part_if;
     r.dpos_bias = a->dpos_bias; r.dscale_embed = a->dscale_embed;
     r.dscore_gain = a->dscore_gain; r.dif_gain = a->dif_gain;
+    r.se_stage = a->dscale_embed ? reinterpret_cast<float*>(ws + L.se_stage) : nullptr;
+    r.se_slices = rows ? L.se_slices : 0;
+    r.se_per = L.se_per;
     if ((st = hip_status(launch_bwd_reduce(r, hs)))) return st;
   }
   return DSQG_OK;

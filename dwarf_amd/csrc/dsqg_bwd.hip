@@ -62,13 +62,30 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
     t -= r.H;
   }
   if (r.dscale_embed && t < r.J * r.D) {
-    const long long nb = (long long)r.B * r.H * r.n_chunks;
     const long long stride = (long long)r.J * r.D;
     float s = 0.f;
-    for (long long blk = lane; blk < nb; blk += 64) s += r.part_se[blk * stride + t];
+    for (int k = lane; k < r.se_slices; k += 64) s += r.se_stage[k * stride + t];
     s = wave_sum_fixed(s);
     if (lane == 0) r.dscale_embed[t] = s;
   }
+}
+
+// First stage of the dscale_embed sum: workgroup (x, y) sums, for 256 consecutive elements of
+// [J*D], the partials of workgroups [y*se_per, (y+1)*se_per) in order.  A partial row is read
+// in 1 KB runs (one float per lane, consecutive elements), not as one float per partial row
+// per lane; the final per-element sum then reads only se_slices values.
+__global__ __launch_bounds__(kBlock) void bwd_reduce_se_stage_kernel(ReduceParams r) {
+  const long long JD = (long long)r.J * r.D;
+  const long long t = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (t >= JD) return;
+  const long long nb = (long long)r.B * r.H * r.n_chunks;
+  const long long b0 = (long long)blockIdx.y * r.se_per;
+  const long long b1 = b0 + r.se_per < nb ? b0 + r.se_per : nb;
+  const float* src = r.part_se + t;
+  float acc = 0.f;
+#pragma unroll 8
+  for (long long blk = b0; blk < b1; ++blk) acc += src[blk * JD];
+  r.se_stage[blockIdx.y * JD + t] = acc;
 }
 
 bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
@@ -88,7 +105,7 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
   p.n_tiles = (p.N + QPB - 1) / QPB;
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
   const long long work = (long long)p.B * p.H * p.n_tiles;
-  const long long target = se_grad ? 1024 : 4096;
+  const long long target = se_grad ? 2048 : 4096;
   int tpb = (int)((work + target - 1) / target);
   if (tpb < 1) tpb = 1;
   if (tpb > p.n_tiles) tpb = p.n_tiles > 0 ? p.n_tiles : 1;
@@ -97,6 +114,13 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
 }
 
 hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st) {
+  if (r.dscale_embed && r.se_slices > 0) {
+    const long long JD = (long long)r.J * r.D;
+    hipLaunchKernelGGL(bwd_reduce_se_stage_kernel, dim3((unsigned)((JD + kBlock - 1) / kBlock), (unsigned)r.se_slices),
+                       dim3(kBlock), 0, st, r);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const long long total = 2LL * r.J * r.H + r.H + (long long)r.J * r.D;  // outputs (upper bound)
   if (total == 0) return hipSuccess;
   const long long waves_per_block = kBlock / 64;

@@ -25,7 +25,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel(BwdParams p) {
   constexpr int KT = 64;                  // key rows per workgroup
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
@@ -36,20 +36,24 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
   constexpr int CHW = D / 32;             // 16-byte chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;
-  constexpr int TS = 52;                  // [query][tap] table row stride
+  // [query][dense tap] table row stride: a 36-word pitch spreads the band's diagonal reads
+  // (row 4g + r, tap 4g + r - i) over all 64 banks.
+  constexpr int TS = 35;
   constexpr int SEJ = 48;
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sQ[WIN * RV];
   __shared__ __align__(16) bf16_t sO[WIN * RV];
-  __shared__ __align__(16) bf16_t sQs[4][16 * RV];   // wave-private long-range query rows
-  __shared__ __align__(16) bf16_t sOs[4][16 * RV];   // ... and their dOut rows
+  // Wave-private long-range query / dOut rows.  With scale_embed they reuse the window tiles
+  // once the band is done (the LDS then fits three workgroups per CU).
+  __shared__ __align__(16) bf16_t sQs[HAS_SE ? 8 : 4 * 16 * RV];
+  __shared__ __align__(16) bf16_t sOs[HAS_SE ? 8 : 4 * 16 * RV];
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
-  __shared__ float sT[HAS_SE ? WIN * TS : 1];        // log2e (bias + c q.se) per window query, tap
+  __shared__ float sT[HAS_SE ? WIN * TS : 1];        // log2e (bias + c q.se), window query x dense tap
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain2[kMaxTaps];                 // gain * c * log2e
   __shared__ float sGainC[kMaxTaps];                 // gain * c
-  __shared__ float4 sTrip[4][16];                    // per wave: long-range (q.k, dOut.v, T) of one tap
+  __shared__ float2 sPair[4][16];                    // per wave: long-range (score, dOut.v) of one tap
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -115,17 +119,19 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
       lq[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
       dq_[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
     }
-  // lse and D' of the query on this lane's diagonal for every long-range tap (query m + delta;
-  // lanes off the diagonal fetch a harmless value), requested before the tap loop.
-  float lseS[NSM], dpS[NSM];
+  // lse and D' of the query on this lane's diagonal for the long-range taps (query m + delta;
+  // lanes off the diagonal fetch a harmless value): all of them before the tap loop, or with
+  // scale_embed (fewer free registers) in a ring LPF taps ahead, like the query rows.
+  constexpr int LPF = HAS_SE ? PF : NSM;
+  float lseS[LPF], dpS[LPF];
+  auto load_lse = [&](int t) {
+    const int nq = m + p.taps.delta[W + 1 + t];
+    lseS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
+    dpS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
+  };
 #pragma unroll
-  for (int t = 0; t < NSM; ++t) {
-    if (NSC > 0 || t < NS) {
-      const int nq = m + p.taps.delta[W + 1 + t];
-      lseS[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
-      dpS[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
-    }
-  }
+  for (int t = 0; t < LPF; ++t)
+    if (NSC > 0 ? t < NSC : t < NS) load_lse(t);
   // Long-range query / dOut rows m0w + delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
   uint4 qS[PF][CHW], oS[PF][CHW];
 #pragma unroll
@@ -163,6 +169,29 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
   }
   __syncthreads();
 
+  if constexpr (HAS_SE) {
+    // T[row][j] = log2e (bias_j + c q.se_j) for the 96 window queries (Q SE^T) and the dense
+    // taps j <= W, 16-row blocks w and w+4 per wave (before the band's accumulators are live).
+    for (int blk = w; blk < WIN / 16; blk += 4) {
+      const bf16_t* qr = sQ + (16 * blk + i) * RV + 8 * g;
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        f32x4_t acc = zero4();
+        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * s)),
+                              as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), acc);
+        const int j = 16 * jb + i;  // column = tap, rows = queries 4g + r
+        if (j <= W) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sT[(16 * blk + 4 * g + r) * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
   // ---- Dense band: S = Q K^T, U = dOut V^T for query blocks qb = 0..2. ----
   f32x4_t accS[3], accU[3];
 #pragma unroll
@@ -177,29 +206,6 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
       accU[qb] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(orr + 32 * s)), vB[s], accU[qb]);
     }
   }
-  if constexpr (HAS_SE) {
-    // T[row][j] = log2e (bias_j + c q.se_j) for the 96 window queries (Q SE^T), 16-row blocks
-    // w and w+4 per wave.
-    for (int blk = w; blk < WIN / 16; blk += 4) {
-      const bf16_t* qr = sQ + (16 * blk + i) * RV + 8 * g;
-#pragma unroll
-      for (int jb = 0; jb < 3; ++jb) {
-        f32x4_t acc = zero4();
-        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(qr + 32 * s)),
-                              as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), acc);
-        const int j = 16 * jb + i;  // column = tap, rows = queries 4g + r
-        if (j < J) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) sT[(16 * blk + 4 * g + r) * TS + j] = fmaf(c2, acc[r], sBias2[j]);
-        }
-      }
-    }
-    __syncthreads();
-  }
-
   f32x4_t dK[DB], dV[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) { dK[db] = zero4(); dV[db] = zero4(); }
@@ -232,8 +238,9 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
 
   // ---- Long-range taps: queries m0w + delta + 0..15, diagonal of one tile each. ----
   const bool diag = g == (i >> 2);
-  bf16_t* qsw = sQs[w];
-  bf16_t* osw = sOs[w];
+  bf16_t* qsw = (HAS_SE ? sQ : sQs) + w * 16 * RV;
+  bf16_t* osw = (HAS_SE ? sO : sOs) + w * 16 * RV;
+  if constexpr (HAS_SE) __syncthreads();  // every wave's band reads of sQ / sO are done
   const bf16_t* qtr = qsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
   const bf16_t* otr = osw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
@@ -241,23 +248,27 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
       const int dl = p.taps.delta[j];
-      // q.k, dOut.v (and q.se_j) on the VALU: each lane dots its 16-byte chunk, the row's lanes
-      // sum (DPP), and one lane per row hands the results to the diagonal lane through LDS.
-      // The query / dOut rows are staged (natural row order) for the transposing reads.
+      // This tap's lse / D' (taken before the ring slot is refilled for tap t + PF).
+      const float lseq = lseS[t % LPF], dpq = dpS[t % LPF];
+      // The score's dot products (gain c log2e q.k + c log2e q.se_j) and dOut.v on the VALU:
+      // each lane dots its 16-byte chunk, the row's lanes sum (DPP), and one lane per row hands
+      // the pair to the diagonal lane through LDS.  The query / dOut rows are staged (natural
+      // row order) for the transposing reads.
 #pragma unroll
       for (int u = 0; u < CHW; ++u) {
-        const float dk = group_sum<CPR>(dot8_bf16(qS[t % PF][u], kR[u], 0.f));
-        const float dv = group_sum<CPR>(dot8_bf16(oS[t % PF][u], vR[u], 0.f));
-        float tqr = sBias2[j];  // log2e (bias + c q.se) for this query row
+        float sk = sGain2[j] * dot8_bf16(qS[t % PF][u], kR[u], 0.f);
         if constexpr (HAS_SE) {
           const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
-          tqr = fmaf(c2, group_sum<CPR>(dot8_bf16(qS[t % PF][u], se, 0.f)), tqr);
+          sk = fmaf(c2, dot8_bf16(qS[t % PF][u], se, 0.f), sk);
         }
+        const float dk = group_sum<CPR>(sk);
+        const float dv = group_sum<CPR>(dot8_bf16(oS[t % PF][u], vR[u], 0.f));
         st16(qsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qS[t % PF][u]);
         st16(osw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, oS[t % PF][u]);
-        if (rc_chunk<D>(l, u) == 0) sTrip[w][rc_row<D>(l, u)] = float4{dk, dv, tqr, 0.f};
+        if (rc_chunk<D>(l, u) == 0) sPair[w][rc_row<D>(l, u)] = float2{dk, dv};
       }
       if (t + PF < NS) {
+        if constexpr (HAS_SE) load_lse(t + PF);
         const int n0 = m0w + p.taps.delta[W + 1 + t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
@@ -267,12 +278,11 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dkdv_mfma_kernel(BwdParams p) {
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and results are written
       __builtin_amdgcn_wave_barrier();
-      const float4 tr = sTrip[w][i];
+      const float2 pr = sPair[w][i];
       const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
-      const float lseq = lseS[t], dpq = dpS[t];
       const bool ok = diag && key_ok && nq < N;
-      const float raw = tr.x, uval = tr.y, tq = tr.z;
-      const float alpha = ok ? __builtin_amdgcn_exp2f(fmaf(sGain2[j], raw, tq) - lseq) : 0.f;
+      const float uval = pr.y;
+      const float alpha = ok ? __builtin_amdgcn_exp2f(pr.x + sBias2[j] - lseq) : 0.f;
       const float dS = a * alpha * (uval - dpq);
       const s16x4_t bk = onehot_bf16x4(sGainC[j] * dS, i & 3);
       const s16x4_t bv = onehot_bf16x4(a * alpha, i & 3);

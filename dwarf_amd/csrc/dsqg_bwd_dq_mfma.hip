@@ -14,7 +14,11 @@
 // The dense band and the long-range taps are laid out as in the forward (dsqg_fwd_mfma.hip):
 // band keys [n0w-32, n0w+16) as three 16x16 tiles, long-range taps as the diagonal of one tile.
 // dS is then written to a per-wave [query][tap] table in LDS, from which the workgroup sums
-// dbias (and dg, da) in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS).
+// dbias (and dg, da) in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS over
+// the tile's 64 queries, its [D x J] output tiles split over the four waves).
+// With scale_embed the q.se_j term of the dense taps is an MFMA (SE Q^T) filed in a per-wave
+// [query][tap] table that shares the wave's staging block; for the long-range taps it is a VALU
+// dot product folded into the score, like q.k.
 //
 // Follows _compute_D_v3 + _bwd_dq_v3 (kernels/dsqg_attention_v3.py:170-275), except that D' is
 // computed from the fp32 weights and the parameter gradients avoid atomics.
@@ -25,7 +29,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int QT = 64;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
@@ -37,23 +41,29 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;                   // long-range K/V operands loaded ahead of use
   constexpr int TS = 52;                  // row stride of the per-wave [query][tap] tables (16 B aligned)
+  constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
+  constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
   constexpr int SEJ = 48;                 // scale_embed rows staged (J <= 48)
-  constexpr int SE_PER_T = (SEJ * D + kBlock - 1) / kBlock;
+  constexpr int NTSE = 3 * DB;            // 16x16 tiles of dse^T [D x 48]
+  constexpr int TPW = (NTSE + 3) / 4;     // ... per wave
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sK[WIN * RV];        // dense-window K rows
   __shared__ __align__(16) bf16_t sV[WIN * RV];        // dense-window V rows
-  __shared__ __align__(16) bf16_t sKs[4][16 * RV];     // wave-private long-range K block
-  __shared__ __align__(16) bf16_t sQ[HAS_SE ? 4 * 16 * RV : 8];   // wave's Q rows (for dse)
+  // Wave-private staging block: with scale_embed first the dense-tap table
+  // T[i][j] = log2e (bias_j + c q_i.se_j), then the long-range K rows, then the wave's Q rows
+  // (read by every wave for dse).
+  __shared__ __align__(16) bf16_t sKs[4][HAS_SE ? KSB : 16 * RV];
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];     // scale_embed rows, bf16
-  __shared__ float sT[HAS_SE ? 4 * 16 * TS : 1];       // log2e * (bias + c q.se)
   __shared__ __align__(16) float sDS[4 * 16 * TS];      // dS[query][tap] per wave
   __shared__ float sRAW[4 * 16 * TS];                   // c q.k per (query, tap), for dg
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain2[kMaxTaps];                    // gain * c * log2e
   __shared__ float sGain[kMaxTaps];
   __shared__ float sDp[4 * 16];
-  __shared__ float2 sPair[4][16];                       // per wave: long-range (q.k, dOut.v) of one tap
+  // Per wave, one long-range tap's row results: (q.k, dOut.v), or with scale_embed
+  // (score less bias, dOut.v, q.k, -).
+  __shared__ __align__(16) float sPair[4][16][HAS_SE ? 4 : 2];
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -107,16 +117,14 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   }
 
   float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
-  f32x4_t accSE[HAS_SE ? 3 : 1][HAS_SE ? DB : 1];
+  f32x4_t accSE[HAS_SE ? TPW : 1];  // this wave's dse^T tiles w, w+4, ...
 #pragma unroll
-  for (int jb = 0; jb < (HAS_SE ? 3 : 1); ++jb)
-#pragma unroll
-    for (int db = 0; db < (HAS_SE ? DB : 1); ++db) accSE[jb][db] = zero4();
+  for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
 
   float* sDSw = sDS + w * 16 * TS;
   float* sRAWw = sRAW + w * 16 * TS;
-  float* sTw = sT + (HAS_SE ? w * 16 * TS : 0);
   bf16_t* sKsw = sKs[w];
+  float* sTw = reinterpret_cast<float*>(sKsw);
   const int t_begin = chunk * p.tiles_per_block;
   const int t_end = min(p.n_tiles, t_begin + p.tiles_per_block);
 
@@ -171,12 +179,6 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
         st16(sV + (ci / CPR) * RV + (ci % CPR) * 8, wv[u]);
       }
     }
-    if constexpr (HAS_SE) {
-      // The wave's Q rows (B layout: row i, chunks 8g + 32s) as natural rows, for dse.
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        *reinterpret_cast<bf16x8_t*>(sQ + (w * 16 + i) * RV + 8 * g + 32 * s) = qB[s];
-    }
     __syncthreads();
 
     // ---- Dense band: S^T = K Q^T, U^T = V dOut^T. ----
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * jb + 4 * g + r;
-          if (j < J) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+          if (j <= W) sTw[i * TST + j] = fmaf(c2, acc[r], sBias2[j]);
         }
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
         const int dl = dl0 - 16 * kk - r;
         const bool ok = row_ok && (unsigned)dl <= (unsigned)W && n >= dl;
         const int j = ok ? dl : 0;
-        const float s2 = fmaf(sGain2[j], accS[kk][r], HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+        const float s2 = fmaf(sGain2[j], accS[kk][r], HAS_SE ? sTw[i * TST + j] : sBias2[j]);
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         al[4 * kk + r] = alpha;
         uu[4 * kk + r] = accU[kk][r];
@@ -269,14 +271,26 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
       if (NSC > 0 || t < NS) {
         const int j = W + 1 + t;
         // q.k and dOut.v on the VALU: each lane dots its 16-byte chunk, the row's lanes sum
-        // (DPP), and one lane per row hands the pair to the diagonal lane through LDS.  The key
-        // rows are staged (natural row order) for the transposing reads of X and Y.
+        // (DPP), and one lane per row hands the results to the diagonal lane through LDS.  The
+        // key rows are staged (natural row order) for the transposing reads of X and Y.  With
+        // scale_embed the score (gain c log2e q.k + c log2e q.se_j) is summed as one, and q.k
+        // only for dg.
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
-          const float dk = group_sum<CPR>(dot8_bf16(qR[u], kS[t % PF][u], 0.f));
+          const float qk = dot8_bf16(qR[u], kS[t % PF][u], 0.f);
           const float dv = group_sum<CPR>(dot8_bf16(oR[u], vS[t % PF][u], 0.f));
           st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
-          if (rc_chunk<D>(l, u) == 0) sPair[w][rc_row<D>(l, u)] = float2{dk, dv};
+          if constexpr (HAS_SE) {
+            const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
+            const float sc = group_sum<CPR>(fmaf(c2, dot8_bf16(qR[u], se, 0.f), sGain2[j] * qk));
+            const float raw = g_grad ? group_sum<CPR>(qk) : 0.f;
+            if (rc_chunk<D>(l, u) == 0)
+              *reinterpret_cast<float4*>(sPair[w][rc_row<D>(l, u)]) = float4{sc, dv, raw, 0.f};
+          } else {
+            const float dk = group_sum<CPR>(qk);
+            if (rc_chunk<D>(l, u) == 0)
+              *reinterpret_cast<float2*>(sPair[w][rc_row<D>(l, u)]) = float2{dk, dv};
+          }
         }
         if (t + PF < NS) {
           const int m0 = n0w - p.taps.delta[W + 1 + t + PF];
@@ -288,10 +302,15 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and pairs are written
         __builtin_amdgcn_wave_barrier();
-        const float2 pr = sPair[w][i];
-        const float raw = pr.x, uval = pr.y;
+        float raw, uval, s2;
+        if constexpr (HAS_SE) {
+          const float4 pr = *reinterpret_cast<const float4*>(sPair[w][i]);
+          raw = pr.z; uval = pr.y; s2 = pr.x + sBias2[j];
+        } else {
+          const float2 pr = *reinterpret_cast<const float2*>(sPair[w][i]);
+          raw = pr.x; uval = pr.y; s2 = fmaf(sGain2[j], raw, sBias2[j]);
+        }
         const bool ok = diag && row_ok && n >= p.taps.delta[j];
-        const float s2 = fmaf(sGain2[j], raw, HAS_SE ? sTw[i * TS + j] : sBias2[j]);
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         als[t] = alpha;
         uus[t] = uval;
@@ -310,6 +329,13 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
     }
 
     const float Dp = col_sum(dlane);  // D' = dOut . o (pre-gain o) for query n
+    if constexpr (HAS_SE) {
+      // The wave's Q rows (natural order) replace its K rows, for dse after the tables are done.
+      if (se_grad) {
+#pragma unroll
+        for (int u = 0; u < CHW; ++u) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
+      }
+    }
 
     // ---- dS table [query][tap] (every entry j < J is written: zero where masked). ----
 #pragma unroll
@@ -358,21 +384,27 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
       if (g == 0) p.dpre[rowbase + n] = Dp;
     }
 
-    // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j), per wave.
+    __syncthreads();  // all waves' tables (and Q rows) are complete
+    // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j) over the tile's 64
+    // queries; wave w owns the output tiles w, w+4, ... of the 3 x DB grid.
     if constexpr (HAS_SE) {
       if (se_grad) {
-        const bf16_t* qr = sQ + (w * 16 + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
-        for (int jb = 0; jb < 3; ++jb) {
-          const float* col = sDSw + (4 * g) * TS + 16 * jb + i;
-          const s16x4_t bs = pack_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS]);
+        for (int k = 0; k < TPW; ++k) {
+          const int idx = w + 4 * k;
+          if (idx < NTSE) {
+            const int jb = idx / DB, db = idx - jb * DB;
 #pragma unroll
-          for (int db = 0; db < DB; ++db)
-            accSE[jb][db] = mfma_16x16x16(lds_read_tr16(qr + 16 * db), bs, accSE[jb][db]);
+            for (int ww = 0; ww < 4; ++ww) {
+              const float* col = sDS + (ww * 16 + 4 * g) * TS + 16 * jb + i;
+              const s16x4_t bs = pack_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS]);
+              const bf16_t* qr = sKs[ww] + (4 * g + (i >> 2)) * RV + 4 * (i & 3) + 16 * db;
+              accSE[k] = mfma_16x16x16(lds_read_tr16(qr), bs, accSE[k]);
+            }
+          }
         }
       }
     }
-    __syncthreads();  // all waves' tables are complete
     if (tid < J) {
       float sb = 0.f, sg = 0.f;
       for (int q = 0; q < 64; ++q) {
@@ -397,30 +429,15 @@ __global__ __launch_bounds__(kBlock, 2) void bwd_dq_mfma_kernel(BwdParams p) {
   if (tid == 0 && p.part_if) p.part_if[lb] = acc_if;
   if constexpr (HAS_SE) {
     if (se_grad) {
-      // Reduce the four waves' [d][j] accumulators through LDS (reusing the dS tables), fixed order.
-      __syncthreads();
-      float* red = sDS;  // 4 * 16 * TS floats >= 4 waves * 3 * DB * 64 lanes * 4 values / ...
-      for (int jb = 0; jb < 3; ++jb) {
+      // Lane (i, g) of tile (jb, db) holds dSE^T[d = 16 db + 4 g + r][j = 16 jb + i], r = 0..3.
 #pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          // lane (i, g) holds dSE^T[d = 16db + 4g + r][j = 16jb + i]
-#pragma unroll
-          for (int r = 0; r < 4; ++r) red[(w * 64 + l) * 4 + r] = accSE[jb][db][r];
-          __syncthreads();
-          if (tid < 64) {
-            const int ii = tid & 15, gg = tid >> 4;
-            const int j = 16 * jb + ii;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float sum = 0.f;
-#pragma unroll
-              for (int ww = 0; ww < 4; ++ww) sum += red[(ww * 64 + tid) * 4 + r];
-              const int d = 16 * db + 4 * gg + r;
-              if (j < J) p.part_se[((long long)lb * J + j) * D + d] = c * sum;
-            }
-          }
-          __syncthreads();
-        }
+      for (int k = 0; k < TPW; ++k) {
+        const int idx = w + 4 * k;
+        const int jb = idx / DB, db = idx - jb * DB;
+        const int j = 16 * jb + i;
+        if (idx < NTSE && j < J)
+          *reinterpret_cast<float4*>(p.part_se + ((long long)lb * J + j) * D + 16 * db + 4 * g) =
+              make_float4(c * accSE[k][0], c * accSE[k][1], c * accSE[k][2], c * accSE[k][3]);
       }
     }
   }

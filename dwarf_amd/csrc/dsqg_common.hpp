@@ -163,6 +163,9 @@ struct ReduceParams {
   int B, H, J, D, n_chunks;
   const float* part_bias; const float* part_se; const float* part_gain; const float* part_if;
   float* dpos_bias; float* dscale_embed; float* dscore_gain; float* dif_gain;
+  // dscale_embed is summed in two stages: se_slices runs of se_per consecutive workgroup
+  // partials each, summed column-wise into se_stage [se_slices][J*D], then the slices.
+  float* se_stage; int se_slices, se_per;
 };
 
 struct DecodeParams {

@@ -13,8 +13,10 @@
 //     go through a per-wave LDS table to the lane that owns query i's taps.  An MFMA diagonal
 //     would need the operand order (16 rows x 16 bytes per 16 lanes), which the vector L1
 //     serves at about a quarter of the whole-row rate.
-//  4. Optional q.se_j term: SE Q^T with the same MFMA, kept per wave in an LDS table
-//     T[i][j] = bias[j] + c q_i . se_j; without scale_embed T is the bias row.
+//  4. Optional q.se_j term: for the dense taps SE Q^T with the same MFMA, kept per wave in an
+//     LDS table T[i][j] = bias[j] + c q_i . se_j (in the wave's staging block, which is free
+//     until the output leaves); for the long-range taps a VALU dot product folded into the
+//     score of step 3.  Without scale_embed T is the bias row.
 //  5. Softmax over each query's J taps in registers: the four lanes of a query column combine
 //     max and sum with two cross-lane steps; lse = max + log(sum); the weights are normalised
 //     (and scaled by the IF gain) before P V.
@@ -31,7 +33,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void fwd_mfma_kernel(FwdParams p) {
   constexpr int QT = 64;                  // query rows per workgroup
   constexpr int KS = D / 32;              // 16x16x32 steps over the head dim
   constexpr int DB = D / 16;              // 16-wide head-dim blocks of the output
@@ -43,14 +45,14 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
   static_assert(16 * CPR % 64 == 0, "a wave's 16-row block must split evenly over 64 lanes");
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
-  constexpr int TS = 49;                  // row stride of the per-wave T table
+  constexpr int TS = 38;                  // row stride of the per-wave T table (dense taps; 2-way reads)
+  constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sV[WIN * RV];
   __shared__ __align__(16) bf16_t sK[WIN * RV];   // dense-window K rows (MFMA A operands)
-  __shared__ __align__(16) bf16_t sVs[4][16 * RV];   // wave-private long-range V block
+  __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : 16 * RV];   // wave-private staging block
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
-  __shared__ float sT[HAS_SE ? 4 * 16 * TS : 1];
   __shared__ __align__(16) float sRaw[4][16 * 16];   // per wave: long-range q.k [query][tap]
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
@@ -147,16 +149,24 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
   // (DPP), and one lane per row files the score in the wave's [query][tap] table.  The first
   // half's registers are free before the second half is loaded.
   float* sRw = sRaw[w];
+  // Score of long-range tap t for each of the wave's rows, less the bias (log2 units):
+  // gain c log2e q.k (+ c log2e q.se_j), one DPP sum per row.
+  auto sparse_score = [&](int t) {
+    const int j = W + 1 + t;
 #pragma unroll
-  for (int t = 0; t < NH; ++t) {
-    if (NSC > 0 || t < NS) {
-#pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        const float d = group_sum<CPR>(dot8_bf16(qR[u], kS[t][u], 0.f));
-        if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * 16 + t] = d;
+    for (int u = 0; u < CHW; ++u) {
+      float d = sGain2[j] * dot8_bf16(qR[u], kS[t][u], 0.f);
+      if constexpr (HAS_SE) {
+        const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * (D + 8) + rc_chunk<D>(l, u) * 8);
+        d = fmaf(c2, dot8_bf16(qR[u], se, 0.f), d);
       }
+      d = group_sum<CPR>(d);
+      if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * 16 + t] = d;
     }
-  }
+  };
+#pragma unroll
+  for (int t = 0; t < NH; ++t)
+    if (NSC > 0 || t < NS) sparse_score(t);
 #pragma unroll
   for (int t = NH; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
@@ -180,7 +190,7 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
 
   __builtin_amdgcn_sched_barrier(0);
 
-  float* sTw = sT + (HAS_SE ? w * 16 * TS : 0);
+  float* sTw = reinterpret_cast<float*>(sVs[w]);  // T table until the output exchange
   if constexpr (HAS_SE) {
 #pragma unroll
     for (int jb = 0; jb < 3; ++jb) {
@@ -192,7 +202,7 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * jb + 4 * g + r;
-        if (j < J) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+        if (j <= W) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's table is written
@@ -215,15 +225,8 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
   }
 
 #pragma unroll
-  for (int t = NH; t < NSM; ++t) {
-    if (NSC > 0 || t < NS) {
-#pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        const float d = group_sum<CPR>(dot8_bf16(qR[u], kS[t][u], 0.f));
-        if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * 16 + t] = d;
-      }
-    }
-  }
+  for (int t = NH; t < NSM; ++t)
+    if (NSC > 0 || t < NS) sparse_score(t);
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the table is written
   __builtin_amdgcn_wave_barrier();
   // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(kBlock, 3) void fwd_mfma_kernel(FwdParams p) {
     ss[t] = -INFINITY;
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      const float v = fmaf(sGain2[j], sRw[i * 16 + t], HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+      const float v = sRw[i * 16 + t] + sBias2[j];
       ss[t] = (diag && row_ok && n >= p.taps.delta[j]) ? v : -INFINITY;
     }
   }
