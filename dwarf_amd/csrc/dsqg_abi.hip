@@ -240,7 +240,8 @@ int dsqg_decode_step(const dsqg_decode_args* a, dsqg_stream_t stream) {
   int st = check_shape(s, false, &p.taps);
   if (st) return st;
   if (a->S <= p.taps.maxd) return DSQG_EINVAL;
-  if ((long long)a->S * s.D >= (1LL << 31)) return DSQG_EUNSUPPORTED;  // ring offsets are 32-bit
+  const long long ring_bytes = (long long)a->S * s.D * (s.dtype == DSQG_F32 ? 4 : 2);
+  if (ring_bytes >= (1LL << 31)) return DSQG_EUNSUPPORTED;  // ring byte offsets are 32-bit
   const long long rows = (long long)s.B * s.H;
   if (rows == 0) return DSQG_OK;
   const void* ptrs[] = {a->q, a->k_new, a->v_new, a->k_ring, a->v_ring, a->out};

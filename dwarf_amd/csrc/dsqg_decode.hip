@@ -16,15 +16,18 @@
 // the ring follows README.md:175-177.
 #include "dsqg_common.hpp"
 #include "dsqg_launch.hpp"
+#include "dsqg_mfma.hpp"
 
 namespace dsqg {
 
-// Combine the R lane groups of G = 64/R lanes (lanes l, l^G, l^2G, ...): xor 8 inside a
-// 16-lane row by DPP row_ror:8, xor 16 / xor 32 by v_permlane16/32_swap.  Every lane ends with
+// Combine the R lane groups of G = 64/R lanes (lanes l, l^G, l^2G, ...): xor 4 (G = 4 only)
+// by a lane shuffle, xor 8 inside a 16-lane row by DPP row_ror:8, xor 16 / xor 32 by
+// v_permlane16/32_swap.  Every lane ends with
 // the total; the pairing order is the same on both lanes of each pair.
 template <int R>
 __device__ __forceinline__ float groups_reduce_sum(float x) {
   constexpr int G = 64 / R;
+  if constexpr (G <= 4) x += __shfl_xor(x, 4, 64);                        // lane ^ 4
   if constexpr (G <= 8) x += dpp_f32<0x128>(x);                           // lane ^ 8
   if constexpr (G <= 16) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -36,6 +39,7 @@ __device__ __forceinline__ float groups_reduce_sum(float x) {
 template <int R>
 __device__ __forceinline__ float groups_reduce_max(float x) {
   constexpr int G = 64 / R;
+  if constexpr (G <= 4) x = fmaxf(x, __shfl_xor(x, 4, 64));
   if constexpr (G <= 8) x = fmaxf(x, dpp_f32<0x128>(x));
   if constexpr (G <= 16) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -45,11 +49,39 @@ __device__ __forceinline__ float groups_reduce_max(float x) {
   return fmaxf(__uint_as_float(r2[0]), __uint_as_float(r2[1]));
 }
 
+// Reduce-scatter of the eight per-lane output partials over the lane groups: at each level
+// (lane ^ 32, lane ^ 16 by v_permlane32/16_swap, lane ^ 8 by DPP row_ror:8) a lane keeps half
+// of its values and adds the partner's matching half, so one swap and one add move two values.
+// For D <= 64 every lane ends with one element, index (lane >> 3) & 7 of its 8-element chunk;
+// for D = 128 (four groups) with two, indices 4 (lane >> 5 & 1) + 2 (lane >> 4 & 1) + {0, 1}.
+// A level whose partner lies in the same group (D = 128 at lane ^ 8) is skipped; D = 32 adds
+// the remaining group bit (lane ^ 4) as a plain sum.
+template <int G>
+__device__ __forceinline__ void groups_scatter_sum(float (&a)[8]) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[e]), __float_as_uint(a[e + 4]), false, false);
+    a[e] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[e]), __float_as_uint(a[e + 2]), false, false);
+    a[e] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (G <= 8) {
+    const bool hi = (threadIdx.x & 8) != 0;
+    const float keep = hi ? a[1] : a[0], send = hi ? a[0] : a[1];
+    a[0] = keep + dpp_f32<0x128>(send);  // row_ror:8 = lane ^ 8 inside the 16-lane row
+  }
+  if constexpr (G == 4) a[0] += __shfl_xor(a[0], 4, 64);
+}
+
 template <typename T, int D, int JMAX, bool HAS_SE>
 __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   constexpr int G = D / 8;
   constexpr int R = 64 / G;
   constexpr int P = (JMAX + R - 1) / R;
+  constexpr int E = sizeof(T);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -71,24 +103,29 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     }
     return;
   }
+  if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos + 1;
 
   const T* qrow = static_cast<const T*>(p.q) + bh * D;
   const T* knew = static_cast<const T*>(p.k_new) + bh * D;
   const T* vnew = static_cast<const T*>(p.v_new) + bh * D;
   T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
   T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
+  // Ring reads go through buffer resources over this sequence's ring: a masked tap gets an
+  // offset past the end and reads zeros, so it needs no select in the weighted sum.
+  const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(kring, (short)0, S * D * E, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(vring, (short)0, S * D * E, 0x00020000);
 
   // Two memory round trips per step: everything that does not depend on the position (query,
   // new key/value row, per-tap bias and gain) goes out together with the position itself; the
   // ring rows of the taps follow, all requested before any arithmetic.  Tap 0 (delta = 0) is
-  // the new row, already in registers; so is the row written into the ring at the end.
-  constexpr int C16 = sizeof(T) == 4 ? 2 : 1;  // 16-byte chunks per lane (8 elements)
+  // the new row, already in registers; so is the row written into the ring.
+  constexpr int C16 = E == 4 ? 2 : 1;  // 16-byte chunks per lane (8 elements)
   uint4 qraw[C16], knraw[C16], vnraw[C16];
 #pragma unroll
   for (int u = 0; u < C16; ++u) {
-    qraw[u] = ld16(qrow + d0 + 4 * u * (sizeof(T) == 4));
-    knraw[u] = ld16(knew + d0 + 4 * u * (sizeof(T) == 4));
-    vnraw[u] = ld16(vnew + d0 + 4 * u * (sizeof(T) == 4));
+    qraw[u] = ld16(qrow + d0 + 4 * u * (E == 4));
+    knraw[u] = ld16(knew + d0 + 4 * u * (E == 4));
+    vnraw[u] = ld16(vnew + d0 + 4 * u * (E == 4));
   }
   float pbias[P], pgain[P];
 #pragma unroll
@@ -99,9 +136,16 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     pgain[t] = p.score_gain ? p.score_gain[h * J + jj] : 1.0f;
   }
 
-  // Masked taps (pos - delta < 0) read a valid slot and are zeroed.  Slot of tap delta:
-  // (pos mod S) - delta, wrapped once (0 < delta < S).
+  // Slot of tap delta: (pos mod S) - delta, wrapped once (0 < delta < S).  The new row goes
+  // into slot pos mod S now: no tap of this step reads that slot.
   const int base = (pos >> 31) == 0 ? (int)pos % S : (int)(pos % S);  // 32-bit when it fits
+  if (r == 0) {
+#pragma unroll
+    for (int u = 0; u < C16; ++u) {
+      st16(kring + base * D + d0 + 4 * u * (E == 4), knraw[u]);
+      st16(vring + base * D + d0 + 4 * u * (E == 4), vnraw[u]);
+    }
+  }
   uint4 kraw[P][C16], vraw[P][C16];
   bool ok[P];
 #pragma unroll
@@ -111,11 +155,11 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     ok[t] = j < J && pos - dl >= 0;
     if (dl > 0) {
       const int sw = base - dl;
-      const int sl = ok[t] ? (sw < 0 ? sw + S : sw) : 0;
+      const unsigned off = ok[t] ? (unsigned)(((sw < 0 ? sw + S : sw) * D + d0) * E) : 0x80000000u;
 #pragma unroll
       for (int u = 0; u < C16; ++u) {
-        kraw[t][u] = ld16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4));
-        vraw[t][u] = ld16(vring + sl * D + d0 + 4 * u * (sizeof(T) == 4));
+        kraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rK, off + 16 * u, 0, 0));
+        vraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rV, off + 16 * u, 0, 0));
       }
     } else {
 #pragma unroll
@@ -124,19 +168,24 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   }
 
   float q[8];
-  Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
+  if constexpr (E == 4) Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
   float s[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const int j = t * R + r;
     const int jj = j < J ? j : 0;
-    float kx[8];
-    Vec8<T>::load(reinterpret_cast<const T*>(kraw[t]), kx);
     float pk = 0.f;
+    if constexpr (E == 2) {
+      pk = dot8_bf16(qraw[0], kraw[t][0], 0.f);
+    } else {
+      float kx[8];
+      Vec8<T>::load(reinterpret_cast<const T*>(kraw[t]), kx);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[e], pk);
+      for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[e], pk);
+    }
     float part = pk * pgain[t];
     if constexpr (HAS_SE) {
+      if constexpr (E == 2) Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
 #pragma unroll
       for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[jj * D + d0 + e], part);
     }
@@ -149,6 +198,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   for (int t = 0; t < P; ++t) mx = fmaxf(mx, s[t]);
   mx = groups_reduce_max<R>(mx);
 
+  // Masked taps have weight exp(-inf) = 0 and zero rows; taps j >= J hold the new row (finite).
   float l = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
@@ -159,27 +209,28 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     float vx[8];
     Vec8<T>::load(reinterpret_cast<const T*>(vraw[t]), vx);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, ok[t] ? vx[e] : 0.f, acc[e]);
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(pj, vx[e], acc[e]);
   }
   l = groups_reduce_sum<R>(l);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = groups_reduce_sum<R>(acc[e]);
+  groups_scatter_sum<G>(acc);
 
-  if (r == 0) {
-    const float a = p.if_gain ? p.if_gain[h] : 1.0f;
-    const float inv = a / l;
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = acc[e] * inv;
-    Vec8<T>::store(outrow + d0, o);
-    // The new row goes into slot pos mod S (read by later steps only).
-    const int sl = base;
-#pragma unroll
-    for (int u = 0; u < C16; ++u) {
-      st16(kring + sl * D + d0 + 4 * u * (sizeof(T) == 4), knraw[u]);
-      st16(vring + sl * D + d0 + 4 * u * (sizeof(T) == 4), vnraw[u]);
+  const float a = p.if_gain ? p.if_gain[h] : 1.0f;
+  const float inv = a / l;
+  if constexpr (G == 16) {  // two elements per lane: 4 (lane>>5 & 1) + 2 (lane>>4 & 1) + {0,1}
+    const int e0 = 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1);
+    if constexpr (E == 2) {
+      *reinterpret_cast<unsigned*>(outrow + d0 + e0) =
+          f32_to_bf16(acc[0] * inv) | (f32_to_bf16(acc[1] * inv) << 16);
+    } else {
+      *reinterpret_cast<float2*>(outrow + d0 + e0) = make_float2(acc[0] * inv, acc[1] * inv);
     }
-    if (p.pos_next && h == 0 && g == 0) p.pos_next[b] = pos + 1;
+  } else if (G == 8 || (r & 1) == 0) {  // one element per lane (D = 32: both lanes of a pair hold it)
+    const int e0 = (lane >> 3) & 7;
+    if constexpr (E == 2) {
+      outrow[d0 + e0] = (T)f32_to_bf16(acc[0] * inv);
+    } else {
+      outrow[d0 + e0] = acc[0] * inv;
+    }
   }
 }
 

@@ -112,7 +112,7 @@ typedef struct {
 } dsqg_bwd_args;
 
 /* Decode step: one new token per sequence.  q, k_new, v_new, out are [B,H,D] contiguous;
- * k_ring, v_ring are [B,H,S,D] contiguous rings with S > max(offsets) and S*D < 2^31
+ * k_ring, v_ring are [B,H,S,D] contiguous rings with S > max(offsets) and S*D*sizeof(dtype) < 2^31
  * (DSQG_EUNSUPPORTED otherwise).  pos [B] (device,
  * int64) is the absolute position of the new token.  The step writes k_new / v_new into slot
  * pos mod S, then attends slot (pos - delta_j) mod S for delta_j > 0 and the new row for

@@ -55,19 +55,24 @@ def test_decode_workload_1000_steps(gpu_device):
     assert torch.equal(d["v_ring"].cpu(), v_ring_ref)
 
 
+@pytest.mark.parametrize("D", [32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("p", [0, 7, 40, 1535, 1536, 2500])
-def test_decode_equals_full_sequence_row(gpu_device, dtype, p):
+def test_decode_equals_full_sequence_row(gpu_device, dtype, p, D):
     """After prefilling the ring from a sequence of length p, the step at position p equals
-    row p of the full-sequence forward (taps with p - delta < 0 are masked, not wrapped)."""
-    B, H, D = 3, 2, 64
-    g = torch.Generator().manual_seed(1000 + p)
+    row p of the full-sequence forward (taps with p - delta < 0 are masked, not wrapped).
+    Every head dim: the output's lane layout differs per D."""
+    B, H = 3, 2
+    g = torch.Generator().manual_seed(1000 + p + D)
     qs, ks, vs = (torch.randn(B, H, p + 1, D, generator=g).to(dtype) for _ in range(3))
     pb = torch.randn(44, H, generator=g) * 0.5
     se = torch.randn(44, D, generator=g) * 0.1
     sg = torch.rand(H, 44, generator=g) + 0.5
     a = torch.rand(H, generator=g) * 0.4 + 0.8
     cache = dwarf_amd.DSQGRingCache(B, H, D, OFFSETS_V3, dtype=dtype, device=gpu_device)
+    # Slots no valid tap reads hold NaN: masked taps must not reach the output.
+    cache.k_ring.fill_(float("nan"))
+    cache.v_ring.fill_(float("nan"))
     if p > 0:
         cache.prefill(ks[:, :, :p].to(gpu_device), vs[:, :, :p].to(gpu_device))
     else:
@@ -80,7 +85,8 @@ def test_decode_equals_full_sequence_row(gpu_device, dtype, p):
                        sg.to(cd), a.to(cd))[:, :, p]
     err, scale = _err(out, ref)
     bound = 1e-5 * scale if dtype == torch.float32 else 2e-2 * max(1.0, scale)
-    _say(f"p={p} {dtype}: err {err:.3e} bound {bound:.3e}")
+    _say(f"p={p} D={D} {dtype}: err {err:.3e} bound {bound:.3e}")
+    assert torch.isfinite(out).all()
     assert err <= bound
     assert int(cache.pos[0]) == p + 1
 
