@@ -6,11 +6,13 @@ include/dsqg.h), exposed as torch custom ops (``dwarf::dsqg_fwd``, ``dwarf::dsqg
 """
 
 from .offsets import ALL_OFFSETS, OFFSETS_V3, OFFSETS_J46, OFFSETS_J47
-from .api import (dsqg_attention, dsqg_attention_v2, dsqg_attention_v3, dsqg_attention_backend,
-                  dsqg_attention_with_lse, dsqg_decode_step, DSQGRingCache)
+from .api import (dsqg_attention, dsqg_attention_qkv, dsqg_attention_v2, dsqg_attention_v3,
+                  dsqg_attention_backend, dsqg_attention_with_lse, dsqg_decode_step,
+                  DSQGRingCache)
 from .modules import DSQGAttentionV3, DSQGAttentionQW, DSQGAttentionN_Fused
 
 __all__ = ["ALL_OFFSETS", "OFFSETS_V3", "OFFSETS_J46", "OFFSETS_J47", "dsqg_attention",
+           "dsqg_attention_qkv",
            "dsqg_attention_v2", "dsqg_attention_v3", "dsqg_attention_backend",
            "dsqg_attention_with_lse", "dsqg_decode_step", "DSQGRingCache",
            "DSQGAttentionV3", "DSQGAttentionQW", "DSQGAttentionN_Fused"]

@@ -8,6 +8,12 @@
 * ``dsqg_attention(...)`` -- the general form: any offset table, optional ``score_gain[H,J]``
   multiplying the content term and ``if_gain[H]`` multiplying the output (what
   train/train_2048_condU.py:187 does after the kernel), fused into the kernels.
+* ``dsqg_attention_qkv(qkv, num_heads, ...)`` -- the same on the projection output
+  qkv [B,N,3*H*HD] of train/train_2048_condU.py:169-175: the heads are read in place and the
+  gradient comes back as one [B,N,3*H*HD] tensor.
+
+The output [B,H,N,HD] is stored token-major ([B,N,H,HD] memory), so the callers'
+``out.permute(0, 2, 1, 3).reshape(B, N, H * HD)`` (train/train_2048_condU.py:186) is a view.
 
 Dtype rules: bf16 in -> bf16 out with fp32 arithmetic; fp32 in -> fp32 out, computed in fp32
 (the reference would downcast to bf16, kernels/dsqg_attention_v3.py:452-454); any other
@@ -65,6 +71,32 @@ def dsqg_attention(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
 
     out, _ = ops.dsqg_fwd(q, k, v, pos_bias.float(), f32(scale_embed), f32(score_gain),
                           f32(if_gain), list(offs))
+    return out if out.dtype == orig else out.to(orig)
+
+
+def dsqg_attention_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor,
+                       scale_embed: Optional[Tensor] = None, *,
+                       offsets: Optional[Sequence[int]] = None,
+                       score_gain: Optional[Tensor] = None,
+                       if_gain: Optional[Tensor] = None) -> Tensor:
+    """dsqg_attention on q, k, v = the head views of qkv [B,N,3*H*HD] (the qkv_proj output).
+
+    Same result as ``dsqg_attention(*split_qkv(qkv, num_heads), ...)``; differentiable in qkv
+    and every parameter, with d(qkv) produced as one tensor.
+    """
+    assert qkv.dim() == 3, f"qkv must be [B,N,3*H*HD], got {tuple(qkv.shape)}"
+    offs = validate(offsets) if offsets is not None else default_offsets(pos_bias.shape[0])
+    q, k, v = ops.split_qkv(qkv, num_heads)
+    _check_shapes(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offs)
+    orig = qkv.dtype
+    if orig not in (torch.float32, torch.bfloat16):
+        qkv = qkv.bfloat16()
+
+    def f32(t):
+        return None if t is None else t.float()
+
+    out, _ = ops.dsqg_fwd_qkv(qkv, num_heads, pos_bias.float(), f32(scale_embed),
+                              f32(score_gain), f32(if_gain), list(offs))
     return out if out.dtype == orig else out.to(orig)
 
 

@@ -15,7 +15,8 @@ result beyond rounding:
 
 * q, k, v go to the kernels as strided [B,H,N,HD] views of the projection output [B,N,3D]
   (the kernels take row strides), so the three ``permute(...).contiguous()`` copies of the
-  reference are gone;
+  reference are gone; without K/V injection the gradient of the projection output comes back
+  as one tensor, and the output's head merge is a view (token-major storage);
 * the IF gain is applied inside the forward kernel (fp32, before the bf16 rounding of the
   output) and its gradient comes from the backward kernel.
 """
@@ -28,7 +29,7 @@ from typing import Optional, Sequence, Tuple
 import torch
 from torch import Tensor, nn
 
-from .api import dsqg_attention
+from .api import dsqg_attention, dsqg_attention_qkv
 from .offsets import OFFSETS_V3, validate
 
 
@@ -65,13 +66,15 @@ class _DSQGBase(nn.Module):
                 if_gain: Optional[Tensor]) -> Tensor:
         B, N, D = x.shape
         H, HD = self.num_heads, self.head_dim
-        q, k, v = _heads(self.qkv_proj(x), B, N, H, HD)
-        if kv_inject is not None:
+        qkv = self.qkv_proj(x)
+        if kv_inject is None:
+            out = dsqg_attention_qkv(qkv, H, self.pos_bias, scale_embed, offsets=self._offsets,
+                                     if_gain=if_gain)
+        else:
+            q, k, v = _heads(qkv, B, N, H, HD)
             k_delta, v_delta = kv_inject
-            k = k + k_delta
-            v = v + v_delta
-        out = dsqg_attention(q, k, v, self.pos_bias, scale_embed, offsets=self._offsets,
-                             if_gain=if_gain)
+            out = dsqg_attention(q, k + k_delta, v + v_delta, self.pos_bias, scale_embed,
+                                 offsets=self._offsets, if_gain=if_gain)
         out_flat = out.permute(0, 2, 1, 3).reshape(B, N, D)
         gate = torch.sigmoid(self.gate_proj(x))
         return self.dropout(self.out_proj(out_flat * gate))

@@ -1,4 +1,5 @@
-"""torch custom ops over the C ABI: ``dwarf::dsqg_fwd``, ``dwarf::dsqg_bwd``, ``dwarf::dsqg_decode``.
+"""torch custom ops over the C ABI: ``dwarf::dsqg_fwd``, ``dwarf::dsqg_fwd_qkv``, ``dwarf::dsqg_bwd``,
+``dwarf::dsqg_decode``.
 
 The ops take device tensors, pass raw pointers, element strides and the current HIP stream
 to libdsqg_hip.so through ctypes, and allocate their outputs (and the backward workspace) with
@@ -63,6 +64,21 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _token_major(B: int, H: int, N: int, D: int, **kw) -> Tensor:
+    """A [B,H,N,D] tensor stored token-major ([B,N,H,D] memory): ``.permute(0, 2, 1, 3)
+    .reshape(B, N, H * D)`` of it is a view, so merging the heads costs no copy."""
+    return torch.empty((B, N, H, D), **kw).permute(0, 2, 1, 3)
+
+
+def split_qkv(qkv: Tensor, num_heads: int) -> Tuple[Tensor, Tensor, Tensor]:
+    """q, k, v as [B,H,N,HD] views of a projection output qkv [B,N,3*H*HD] (no copy)."""
+    B, N, E3 = qkv.shape
+    assert E3 % (3 * num_heads) == 0, f"qkv last dim {E3} is not 3 * num_heads * head_dim"
+    HD = E3 // (3 * num_heads)
+    q, k, v = qkv.split(num_heads * HD, dim=-1)
+    return tuple(t.view(B, N, num_heads, HD).permute(0, 2, 1, 3) for t in (q, k, v))
+
+
 # ------------------------------------------------------------------------------------------
 # Forward
 # ------------------------------------------------------------------------------------------
@@ -81,7 +97,7 @@ class FwdLaunch:
                                  f"{q.dtype}/{k.dtype}/{v.dtype}")
         q, k, v = _rows_ready(q), _rows_ready(k), _rows_ready(v)
         pb, se, sg, ig = _param(pos_bias), _param(scale_embed), _param(score_gain), _param(if_gain)
-        self.out = torch.empty((B, H, N, D), dtype=q.dtype, device=dev)
+        self.out = _token_major(B, H, N, D, dtype=q.dtype, device=dev)
         self.lse = torch.empty((B, H, N), dtype=torch.float32, device=dev)
         self._keep = (q, k, v, pb, se, sg, ig)
         a = _lib.FwdArgs()
@@ -102,7 +118,7 @@ class FwdLaunch:
 def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
              scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
              if_gain: Optional[Tensor], offsets: List[int]) -> Tuple[Tensor, Tensor]:
-    """out [B,H,N,D] (dtype of q) and lse [B,H,N] fp32."""
+    """out [B,H,N,D] (dtype of q; token-major storage) and lse [B,H,N] fp32."""
     launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
     launch.run()
     return launch.out, launch.lse
@@ -111,7 +127,27 @@ def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
 @dsqg_fwd.register_fake
 def _(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
     B, H, N, D = q.shape
-    return q.new_empty((B, H, N, D)), q.new_empty((B, H, N), dtype=torch.float32)
+    return q.new_empty((B, N, H, D)).permute(0, 2, 1, 3), q.new_empty((B, H, N), dtype=torch.float32)
+
+
+@torch.library.custom_op("dwarf::dsqg_fwd_qkv", mutates_args=())
+def dsqg_fwd_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor, scale_embed: Optional[Tensor],
+                 score_gain: Optional[Tensor], if_gain: Optional[Tensor],
+                 offsets: List[int]) -> Tuple[Tensor, Tensor]:
+    """dsqg_fwd on the q, k, v head views of one projection output qkv [B,N,3*H*HD]; its
+    gradient is returned as one [B,N,3*H*HD] tensor (no per-head concatenation)."""
+    q, k, v = split_qkv(qkv, num_heads)
+    launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
+    launch.run()
+    return launch.out, launch.lse
+
+
+@dsqg_fwd_qkv.register_fake
+def _(qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets):
+    B, N, E3 = qkv.shape
+    HD = E3 // (3 * num_heads)
+    return (qkv.new_empty((B, N, num_heads, HD)).permute(0, 2, 1, 3),
+            qkv.new_empty((B, num_heads, N), dtype=torch.float32))
 
 
 # ------------------------------------------------------------------------------------------
@@ -129,7 +165,7 @@ class BwdLaunch:
               "params": "dsqg_bwd_params"}
 
     def __init__(self, q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
-                 need_dse, need_dg, need_da):
+                 need_dse, need_dg, need_da, grads=None):
         dev = _require_gpu(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain)
         self.lib = _lib.load()
         self.device = dev
@@ -142,9 +178,9 @@ class BwdLaunch:
         q, k, v, dout = _rows_ready(q), _rows_ready(k), _rows_ready(v), _rows_ready(dout)
         lse = lse.contiguous()
         pb, se, sg, ig = _param(pos_bias), _param(scale_embed), _param(score_gain), _param(if_gain)
-        self.dq = torch.empty((B, H, N, D), dtype=q.dtype, device=dev)
-        self.dk = torch.empty_like(self.dq)
-        self.dv = torch.empty_like(self.dq)
+        if grads is None:  # else (dq, dk, dv) [B,H,N,D] views the caller allocated
+            grads = tuple(torch.empty((B, H, N, D), dtype=q.dtype, device=dev) for _ in range(3))
+        self.dq, self.dk, self.dv = grads
         f32 = dict(dtype=torch.float32, device=dev)
         self.dpos_bias = torch.empty((J, H), **f32)
         self.dscale_embed = torch.empty((J, D) if need_dse else (0,), **f32)
@@ -229,6 +265,63 @@ def _backward(ctx, dout, _dlse):
 
 
 torch.library.register_autograd("dwarf::dsqg_fwd", _backward, setup_context=_setup_context)
+
+
+def _setup_context_qkv(ctx, inputs, output):
+    qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets = inputs
+    _, lse = output
+    ctx.save_for_backward(qkv, lse, pos_bias, scale_embed, score_gain, if_gain)
+    ctx.num_heads = num_heads
+    ctx.offsets = list(offsets)
+    ctx.mark_non_differentiable(lse)
+
+
+def _backward_qkv(ctx, dout, _dlse):
+    qkv, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    need_dse = bool(need[3]) and scale_embed is not None
+    need_dg = bool(need[4]) and score_gain is not None
+    need_da = bool(need[5]) and if_gain is not None
+    dqkv, dpb, dse, dg, da = dsqg_bwd_qkv(qkv, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias,
+                                          scale_embed, score_gain, if_gain, ctx.offsets,
+                                          need_dse, need_dg, need_da)
+    return (dqkv, None, dpb.to(pos_bias.dtype),
+            dse.to(scale_embed.dtype) if need_dse else None,
+            dg.to(score_gain.dtype) if need_dg else None,
+            da.to(if_gain.dtype) if need_da else None, None)
+
+
+@torch.library.custom_op("dwarf::dsqg_bwd_qkv", mutates_args=())
+def dsqg_bwd_qkv(qkv: Tensor, num_heads: int, dout: Tensor, lse: Tensor, pos_bias: Tensor,
+                 scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
+                 if_gain: Optional[Tensor], offsets: List[int], need_dse: bool, need_dg: bool,
+                 need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dqkv [B,N,3*H*HD], dpos_bias, dscale_embed, dscore_gain, dif_gain): dq, dk, dv are
+    written straight into the head views of one gradient buffer."""
+    q, k, v = split_qkv(qkv, num_heads)
+    dqkv = torch.empty_like(qkv, memory_format=torch.contiguous_format)
+    launch = BwdLaunch(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
+                       need_dse, need_dg, need_da, grads=split_qkv(dqkv, num_heads))
+    launch.run()
+    _, _, _, dpb, dse, dg, da = launch.outputs()
+    return dqkv, dpb, dse, dg, da
+
+
+@dsqg_bwd_qkv.register_fake
+def _(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets, need_dse,
+      need_dg, need_da):
+    B, N, E3 = qkv.shape
+    HD = E3 // (3 * num_heads)
+    J = len(offsets)
+    f = dict(dtype=torch.float32)
+    return (qkv.new_empty(qkv.shape), qkv.new_empty((J, num_heads), **f),
+            qkv.new_empty((J, HD) if need_dse else (0,), **f),
+            qkv.new_empty((num_heads, J) if need_dg else (0,), **f),
+            qkv.new_empty((num_heads,) if need_da else (0,), **f))
+
+
+torch.library.register_autograd("dwarf::dsqg_fwd_qkv", _backward_qkv,
+                                setup_context=_setup_context_qkv)
 
 
 # ------------------------------------------------------------------------------------------

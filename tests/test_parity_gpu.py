@@ -268,3 +268,30 @@ def test_fp32_path_does_not_downcast(gpu_device):
     assert out.dtype == torch.float32
     ref = dsqg_forward(*(inp[n].double() for n in ("q", "k", "v", "pos_bias", "scale_embed")))
     check("out fp32", out.cpu(), ref, "fp32")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_qkv_entry_matches_split_heads(gpu_device, dtype):
+    """dsqg_attention_qkv on a [B,N,3*H*D] projection output: the same output, and its one
+    qkv gradient equals the three head gradients of dsqg_attention on the split views, bit
+    for bit (same kernels, same inputs; only the gradient buffer differs)."""
+    B, H, N, D = 2, 4, 333, 64
+    g = torch.Generator().manual_seed(17)
+    qkv0 = torch.randn(B, N, 3 * H * D, generator=g).to(dtype).to(gpu_device)
+    pb0 = (torch.randn(44, H, generator=g) * 0.5).to(gpu_device)
+    se0 = (torch.randn(44, D, generator=g) * 0.1).to(gpu_device)
+    a0 = (0.8 + 0.4 * torch.rand(H, generator=g)).to(gpu_device)
+    dy = torch.randn(B, H, N, D, generator=g).to(dtype).to(gpu_device)
+    res = []
+    for fused in (True, False):
+        qkv, pb, se, a = (t.clone().requires_grad_(True) for t in (qkv0, pb0, se0, a0))
+        if fused:
+            out = dwarf_amd.dsqg_attention_qkv(qkv, H, pb, se, if_gain=a)
+        else:
+            out = dwarf_amd.dsqg_attention(*ops.split_qkv(qkv, H), pb, se, if_gain=a)
+        out.backward(dy)
+        res.append((out.detach(), qkv.grad, pb.grad, se.grad, a.grad))
+    for name, x, y in zip(("out", "dqkv", "dpos_bias", "dscale_embed", "dif_gain"), *res):
+        assert torch.equal(x, y), name
+    # The head merge of the output is a view: [B,H,N,D] stored token-major.
+    assert res[0][0].permute(0, 2, 1, 3).is_contiguous()
