@@ -10,7 +10,12 @@ State dicts saved from the reference modules load unchanged (``load_state_dict(s
 
 Forward semantics follow the reference modules: qkv projection, optional Huygens K/V injection
 (``kv_inject=(k_delta, v_delta)`` added to K and V only), DSQG attention, per-head IF gain
-(QW), ``out_proj(out * sigmoid(gate_proj(x)))`` and dropout.  Differences that change no
+(QW), ``out_proj(out * sigmoid(gate_proj(x)))`` and dropout.
+
+Incremental decoding (no counterpart in the reference, whose generate() re-runs the whole prefix,
+train/train_2048_condU.py:463-487): ``cache = m.new_cache(B)``, ``y = m.prefill(x, cache)``
+(the forward on a prompt, which also loads the layer's K/V ring) and ``y_t = m.step(x_t,
+cache)`` for each new token, one ring-buffer decode step per layer (README.md:175-179).  Differences that change no
 result beyond rounding:
 
 * q, k, v go to the kernels as strided [B,H,N,HD] views of the projection output [B,N,3D]
@@ -29,7 +34,8 @@ from typing import Optional, Sequence, Tuple
 import torch
 from torch import Tensor, nn
 
-from .api import dsqg_attention, dsqg_attention_qkv
+from . import ops
+from .api import DSQGRingCache, dsqg_attention, dsqg_attention_qkv
 from .offsets import OFFSETS_V3, validate
 
 
@@ -63,21 +69,44 @@ class _DSQGBase(nn.Module):
         self.dropout = nn.Dropout(dropout)
 
     def _attend(self, x: Tensor, kv_inject, scale_embed: Optional[Tensor],
-                if_gain: Optional[Tensor]) -> Tensor:
+                if_gain: Optional[Tensor], cache: Optional[DSQGRingCache] = None) -> Tensor:
         B, N, D = x.shape
         H, HD = self.num_heads, self.head_dim
         qkv = self.qkv_proj(x)
         if kv_inject is None:
             out = dsqg_attention_qkv(qkv, H, self.pos_bias, scale_embed, offsets=self._offsets,
                                      if_gain=if_gain)
+            k, v = ops.split_qkv(qkv, H)[1:]
         else:
             q, k, v = _heads(qkv, B, N, H, HD)
             k_delta, v_delta = kv_inject
-            out = dsqg_attention(q, k + k_delta, v + v_delta, self.pos_bias, scale_embed,
-                                 offsets=self._offsets, if_gain=if_gain)
+            k, v = k + k_delta, v + v_delta
+            out = dsqg_attention(q, k, v, self.pos_bias, scale_embed, offsets=self._offsets,
+                                 if_gain=if_gain)
+        if cache is not None:
+            cache.prefill(k.detach(), v.detach())
         out_flat = out.permute(0, 2, 1, 3).reshape(B, N, D)
         gate = torch.sigmoid(self.gate_proj(x))
         return self.dropout(self.out_proj(out_flat * gate))
+
+    @torch.no_grad()
+    def _step(self, x_t: Tensor, cache: DSQGRingCache, kv_inject, scale_embed: Optional[Tensor],
+              if_gain: Optional[Tensor]) -> Tensor:  # generation: no autograd graph
+        B, D = x_t.shape
+        H, HD = self.num_heads, self.head_dim
+        q, k, v = self.qkv_proj(x_t).view(B, 3, H, HD).unbind(1)
+        if kv_inject is not None:
+            k_delta, v_delta = kv_inject
+            k, v = k + k_delta, v + v_delta
+        out = cache.step(q, k, v, self.pos_bias, scale_embed, None, if_gain)
+        gate = torch.sigmoid(self.gate_proj(x_t))
+        return self.dropout(self.out_proj(out.reshape(B, D) * gate))
+
+    def new_cache(self, batch: int, device=None, dtype=None) -> DSQGRingCache:
+        """This layer's K/V ring cache (max offset + 1 slots), in the weights' dtype / device."""
+        w = self.qkv_proj.weight
+        return DSQGRingCache(batch, self.num_heads, self.head_dim, self._offsets,
+                             dtype=dtype or w.dtype, device=device or w.device)
 
     def _summary(self) -> dict:
         with torch.no_grad():
@@ -102,6 +131,14 @@ class DSQGAttentionV3(_DSQGBase):
     def forward(self, x: Tensor, kv_inject=None) -> Tensor:
         return self._attend(x, kv_inject, self.scale_embed, None)
 
+    def prefill(self, x: Tensor, cache: DSQGRingCache, kv_inject=None) -> Tensor:
+        """forward(x) on a prompt [B,N,E]; loads the prompt's K/V rows into ``cache``."""
+        return self._attend(x, kv_inject, self.scale_embed, None, cache)
+
+    def step(self, x_t: Tensor, cache: DSQGRingCache, kv_inject=None) -> Tensor:
+        """Output [B,E] for one new token x_t [B,E] at the cache's position (advances it)."""
+        return self._step(x_t, cache, kv_inject, self.scale_embed, None)
+
     def attn_summary(self) -> dict:
         s = self._summary()
         with torch.no_grad():
@@ -124,6 +161,14 @@ class DSQGAttentionQW(_DSQGBase):
 
     def forward(self, x: Tensor, kv_inject=None) -> Tensor:
         return self._attend(x, kv_inject, self.scale_embed, self.if_gain)
+
+    def prefill(self, x: Tensor, cache: DSQGRingCache, kv_inject=None) -> Tensor:
+        """forward(x) on a prompt [B,N,E]; loads the prompt's K/V rows into ``cache``."""
+        return self._attend(x, kv_inject, self.scale_embed, self.if_gain, cache)
+
+    def step(self, x_t: Tensor, cache: DSQGRingCache, kv_inject=None) -> Tensor:
+        """Output [B,E] for one new token x_t [B,E] at the cache's position (advances it)."""
+        return self._step(x_t, cache, kv_inject, self.scale_embed, self.if_gain)
 
     def attn_summary(self) -> dict:
         s = self._summary()
@@ -148,6 +193,14 @@ class DSQGAttentionN_Fused(_DSQGBase):
 
     def forward(self, x: Tensor) -> Tensor:
         return self._attend(x, None, None, None)
+
+    def prefill(self, x: Tensor, cache: DSQGRingCache) -> Tensor:
+        """forward(x) on a prompt [B,N,E]; loads the prompt's K/V rows into ``cache``."""
+        return self._attend(x, None, None, None, cache)
+
+    def step(self, x_t: Tensor, cache: DSQGRingCache) -> Tensor:
+        """Output [B,E] for one new token x_t [B,E] at the cache's position (advances it)."""
+        return self._step(x_t, cache, None, None, None)
 
     def attn_summary(self) -> dict:
         return self._summary()

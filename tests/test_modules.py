@@ -142,3 +142,43 @@ def test_module_kv_inject(gpu_device):
     y = mg(x.to(gpu_device), kv_inject=(kd.to(gpu_device), vd.to(gpu_device)))
     err = (y.detach().cpu() - ref.detach()).abs().max().item()
     assert err <= 1e-4 * ref.abs().max().item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("cls,dtype,N0", [("QW", torch.float32, 70), ("QW", torch.bfloat16, 70),
+                                          ("V3", torch.bfloat16, 1600), ("N", torch.float32, 40)])
+def test_module_prefill_then_steps_equal_forward(gpu_device, cls, dtype, N0):
+    """prefill on N0 prompt tokens, then one decode step per token, equals the module's forward
+    on the whole sequence, row by row (N0 = 1600 wraps the 1537-slot ring).  QW also checks the
+    K/V injection at every step.  Tolerance: fp32 1e-4 of max|y|; bf16 3e-2 * max(1, max|y|)."""
+    torch.manual_seed(23)
+    E, H, B, T = 256, 4, 2, 4
+    m = {"V3": DSQGAttentionV3, "QW": DSQGAttentionQW, "N": DSQGAttentionN_Fused}[cls](E, H, dropout=0.0)
+    with torch.no_grad():
+        m.pos_bias.add_(0.3 * torch.randn_like(m.pos_bias))
+        if hasattr(m, "scale_embed"):
+            m.scale_embed.copy_(0.5 * torch.randn_like(m.scale_embed))
+        if hasattr(m, "if_gain"):
+            m.if_gain.copy_(0.8 + 0.4 * torch.rand_like(m.if_gain))
+    m = m.to(gpu_device, dtype).eval()
+    x = torch.randn(B, N0 + T, E, device=gpu_device, dtype=dtype)
+    inject = cls == "QW"
+    kd = (0.5 * torch.randn(B, H, N0 + T, E // H, device=gpu_device)).to(dtype) if inject else None
+    vd = (0.5 * torch.randn(B, H, N0 + T, E // H, device=gpu_device)).to(dtype) if inject else None
+    with torch.no_grad():
+        full = m(x, kv_inject=(kd, vd)) if inject else m(x)
+        cache = m.new_cache(B)
+        pre = (m.prefill(x[:, :N0], cache, kv_inject=(kd[:, :, :N0], vd[:, :, :N0])) if inject
+               else m.prefill(x[:, :N0], cache))
+        steps = [m.step(x[:, t], cache, kv_inject=(kd[:, :, t], vd[:, :, t])) if inject
+                 else m.step(x[:, t], cache) for t in range(N0, N0 + T)]
+    ref = full.float()
+    scale = ref.abs().max().item()
+    tol = 1e-4 * scale if dtype == torch.float32 else 3e-2 * max(1.0, scale)
+    # The prompt part differs from the full forward only by the projections' GEMM shapes.
+    err_pre = (pre.float() - ref[:, :N0]).abs().max().item()
+    assert err_pre <= tol, f"{cls} {dtype} N0={N0}: prefill err {err_pre:.3g} > {tol:.3g}"
+    got = torch.stack(steps, dim=1).float()
+    err = (got - ref[:, N0:]).abs().max().item()
+    assert err <= tol, f"{cls} {dtype} N0={N0}: step err {err:.3g} > {tol:.3g}"
+    assert int(cache.pos[0]) == N0 + T
