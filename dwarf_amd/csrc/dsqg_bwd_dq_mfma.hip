@@ -384,7 +384,26 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
       if (g == 0) p.dpre[rowbase + n] = Dp;
     }
 
-    __syncthreads();  // all waves' tables (and Q rows) are complete
+    // dbias / dg column sums of this wave's 16 table rows (its own writes, complete above),
+    // and the wave's sum of D' (for da): one partial row per wave, no workgroup barrier.
+    if (l < J) {
+      float sb = 0.f, sg = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float ds = sDSw[r * TS + l];
+        sb += ds;
+        sg = fmaf(ds, sRAWw[r * TS + l], sg);
+      }
+      acc_bias += sb;
+      acc_gain += sg;
+    }
+    if (l == 0) {
+      float sa = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sa += sDp[w * 16 + r];
+      acc_if += sa;
+    }
+    if constexpr (HAS_SE) __syncthreads();  // all waves' tables (and Q rows) are complete
     // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j) over the tile's 64
     // queries; wave w owns the output tiles w, w+4, ... of the 3 x DB grid.
     if constexpr (HAS_SE) {
@@ -405,28 +424,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
         }
       }
     }
-    if (tid < J) {
-      float sb = 0.f, sg = 0.f;
-      for (int q = 0; q < 64; ++q) {
-        const float ds = sDS[q * TS + tid];  // wave q/16, query q%16: [w][i] rows are contiguous
-        sb += ds;
-        sg = fmaf(ds, sRAW[q * TS + tid], sg);
-      }
-      acc_bias += sb;
-      acc_gain += sg;
-    }
-    if (tid == 0) {
-      float sa = 0.f;
-      for (int q = 0; q < 64; ++q) sa += sDp[q];
-      acc_if += sa;
-    }
   }
 
-  if (tid < J) {
-    p.part_bias[(long long)lb * J + tid] = acc_bias;
-    if (g_grad) p.part_gain[(long long)lb * J + tid] = acc_gain;
+  const long long prow = (long long)lb * (kBlock / 64) + w;  // this wave's partial row
+  if (l < J) {
+    p.part_bias[prow * J + l] = acc_bias;
+    if (g_grad) p.part_gain[prow * J + l] = acc_gain;
   }
-  if (tid == 0 && p.part_if) p.part_if[lb] = acc_if;
+  if (l == 0 && p.part_if) p.part_if[prow] = acc_if;
   if constexpr (HAS_SE) {
     if (se_grad) {
       // Lane (i, g) of tile (jb, db) holds dSE^T[d = 16 db + 4 g + r][j = 16 jb + i], r = 0..3.
