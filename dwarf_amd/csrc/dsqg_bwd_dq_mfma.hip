@@ -28,8 +28,11 @@
 
 namespace dsqg {
 
+// Row stride of the per-wave [query][tap] tables (floats; 16 B aligned rows, 48 taps).
+constexpr int kDqTableStride = 48;
+
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int QT = 64;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
@@ -40,7 +43,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
   constexpr int CHW = D / 32;             // 16-byte chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;                   // long-range K/V operands loaded ahead of use
-  constexpr int TS = 52;                  // row stride of the per-wave [query][tap] tables (16 B aligned)
+  constexpr int TS = kDqTableStride;
   constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
   constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
   constexpr int SEJ = 48;                 // scale_embed rows staged (J <= 48)
@@ -56,11 +59,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
   __shared__ __align__(16) bf16_t sKs[4][HAS_SE ? KSB : 16 * RV];
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];     // scale_embed rows, bf16
   __shared__ __align__(16) float sDS[4 * 16 * TS];      // dS[query][tap] per wave
-  __shared__ float sRAW[4 * 16 * TS];                   // c q.k per (query, tap), for dg
+  // c q.k per (query, tap), for dg only: dynamic LDS, present when score_gain's gradient is
+  // requested (without it the workgroup fits three per CU).
+  extern __shared__ __align__(16) float sDyn[];
+  float* const sRAW = sDyn;
   __shared__ float sBias2[kMaxTaps];
-  __shared__ float sGain2[kMaxTaps];                    // gain * c * log2e
   __shared__ float sGain[kMaxTaps];
-  __shared__ float sDp[4 * 16];
   // Per wave, one long-range tap's row results: (q.k, dOut.v), or with scale_embed
   // (score less bias, dOut.v, q.k, -).
   __shared__ __align__(16) float sPair[4][16][HAS_SE ? 4 : 2];
@@ -98,7 +102,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
   for (int j = tid; j < J; j += kBlock) {
     const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
     sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
-    sGain2[j] = gj * c2;
     sGain[j] = gj;
   }
   if constexpr (HAS_SE) {
@@ -113,7 +116,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
   for (int e = tid; e < 4 * 16 * (48 - J); e += kBlock) {
     const int row = e / (48 - J), j = J + e % (48 - J);
     sDS[row * TS + j] = 0.f;
-    sRAW[row * TS + j] = 0.f;
+    if (g_grad) sRAW[row * TS + j] = 0.f;
   }
 
   float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
@@ -122,11 +125,15 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
   for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
 
   float* sDSw = sDS + w * 16 * TS;
-  float* sRAWw = sRAW + w * 16 * TS;
+  float* sRAWw = sRAW + w * 16 * TS;  // dereferenced only when g_grad
+  // The wave's 16 values of D' go through its own hand-off block once the tap loop is over.
+  float* sDpw = &sPair[w][0][0];
   bf16_t* sKsw = sKs[w];
   float* sTw = reinterpret_cast<float*>(sKsw);
   const int t_begin = chunk * p.tiles_per_block;
-  const int t_end = min(p.n_tiles, t_begin + p.tiles_per_block);
+  // Without scale_embed the plan gives one tile per workgroup (checked at launch): a loop of
+  // one trip keeps the compiler from holding loop-invariant addresses across tiles.
+  const int t_end = HAS_SE ? min(p.n_tiles, t_begin + p.tiles_per_block) : t_begin + 1;
 
   for (int tile = t_begin; tile < t_end; ++tile) {
     const int n0 = tile * QT;
@@ -225,14 +232,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
         const int dl = dl0 - 16 * kk - r;
         const bool ok = row_ok && (unsigned)dl <= (unsigned)W && n >= dl;
         const int j = ok ? dl : 0;
-        const float s2 = fmaf(sGain2[j], accS[kk][r], HAS_SE ? sTw[i * TST + j] : sBias2[j]);
+        const float s2 = fmaf(sGain[j] * c2, accS[kk][r], HAS_SE ? sTw[i * TST + j] : sBias2[j]);
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         al[4 * kk + r] = alpha;
         uu[4 * kk + r] = accU[kk][r];
         dlane = fmaf(alpha, accU[kk][r], dlane);
         wlane += alpha;
         // c q.k for dg goes to the table now (frees the score registers for the taps loop).
-        if ((unsigned)dl <= (unsigned)W) sRAWw[i * TS + dl] = c * accS[kk][r];
+        if (g_grad && (unsigned)dl <= (unsigned)W) sRAWw[i * TS + dl] = c * accS[kk][r];
       }
     }
     const float wsum = col_sum(wlane);
@@ -282,7 +289,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
           st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
           if constexpr (HAS_SE) {
             const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
-            const float sc = group_sum<CPR>(fmaf(c2, dot8_bf16(qR[u], se, 0.f), sGain2[j] * qk));
+            const float sc = group_sum<CPR>(fmaf(c2, dot8_bf16(qR[u], se, 0.f), sGain[j] * c2 * qk));
             const float raw = g_grad ? group_sum<CPR>(qk) : 0.f;
             if (rc_chunk<D>(l, u) == 0)
               *reinterpret_cast<float4*>(sPair[w][rc_row<D>(l, u)]) = float4{sc, dv, raw, 0.f};
@@ -308,13 +315,13 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
           raw = pr.z; uval = pr.y; s2 = pr.x + sBias2[j];
         } else {
           const float2 pr = *reinterpret_cast<const float2*>(sPair[w][i]);
-          raw = pr.x; uval = pr.y; s2 = fmaf(sGain2[j], raw, sBias2[j]);
+          raw = pr.x; uval = pr.y; s2 = fmaf(sGain[j] * c2, raw, sBias2[j]);
         }
         const bool ok = diag && row_ok && n >= p.taps.delta[j];
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         als[t] = alpha;
         uus[t] = uval;
-        if (diag) sRAWw[i * TS + j] = c * raw;
+        if (g_grad && diag) sRAWw[i * TS + j] = c * raw;
         dlane = fmaf(alpha, uval, dlane);
         const float gal = sGain[j] * alpha;
         const s16x4_t b1 = onehot_bf16x4(gal * (uval - D0), i & 3);
@@ -355,7 +362,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
           sDSw[i * TS + W + 1 + t] = a * als[t] * (uus[t] - Dp);
         }
     }
-    if (g == 0) sDp[w * 16 + i] = row_ok ? Dp : 0.f;
+    if (g == 0) sDpw[i] = row_ok ? Dp : 0.f;
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
 
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
       for (int r = 0; r < 16; ++r) {
         const float ds = sDSw[r * TS + l];
         sb += ds;
-        sg = fmaf(ds, sRAWw[r * TS + l], sg);
+        if (g_grad) sg = fmaf(ds, sRAWw[r * TS + l], sg);
       }
       acc_bias += sb;
       acc_gain += sg;
@@ -400,7 +407,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
     if (l == 0) {
       float sa = 0.f;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sa += sDp[w * 16 + r];
+      for (int r = 0; r < 16; ++r) sa += sDpw[r];
       acc_if += sa;
     }
     if constexpr (HAS_SE) __syncthreads();  // all waves' tables (and Q rows) are complete
@@ -450,19 +457,24 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 2) void bwd_dq_mfma_kernel(B
 
 template <int D, bool HAS_SE>
 static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
+  const size_t dyn = p.part_gain ? sizeof(float) * 4 * 16 * kDqTableStride : 0;  // dg table
   switch (p.taps.J - p.taps.W - 1) {
-    case 11: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 11>), dim3(nb), dim3(kBlock), 0, st, p); break;
-    case 13: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 13>), dim3(nb), dim3(kBlock), 0, st, p); break;
-    case 14: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 14>), dim3(nb), dim3(kBlock), 0, st, p); break;
-    default: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 11: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 11>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+    case 13: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 13>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+    case 14: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 14>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+    default: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0>), dim3(nb), dim3(kBlock), dyn, st, p); break;
   }
 }
 
 template <int D>
 static hipError_t launch_dq_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
   // The scale_embed variant also serves dse requested at se = 0.
-  if (p.scale_embed || p.part_se) launch_dq_mfma_ns<D, true>(p, nb, st);
-  else launch_dq_mfma_ns<D, false>(p, nb, st);
+  if (p.scale_embed || p.part_se) {
+    launch_dq_mfma_ns<D, true>(p, nb, st);
+  } else {
+    if (p.tiles_per_block != 1) return hipErrorInvalidValue;  // the single-tile form
+    launch_dq_mfma_ns<D, false>(p, nb, st);
+  }
   return hipGetLastError();
 }
 
