@@ -64,13 +64,12 @@ constexpr size_t kMaxSeSlices = 64;
 BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
   const dsqg_shape& s = a.shape;
   const size_t nb = (size_t)s.B * s.H * p.n_chunks;
-  const size_t nrows = nb * (size_t)p.wg_parts;  // dbias / dg / da partial rows
   BwdLayout L{};
   size_t off = 0;
   L.dpre = off; off = align256(off + sizeof(float) * (size_t)s.B * s.H * s.N);
-  L.part_bias = off; off = align256(off + sizeof(float) * nrows * s.J);
-  L.part_gain = off; if (a.dscore_gain) off = align256(off + sizeof(float) * nrows * s.J);
-  L.part_if = off; if (a.dif_gain) off = align256(off + sizeof(float) * nrows);
+  L.part_bias = off; off = align256(off + sizeof(float) * nb * s.J);
+  L.part_gain = off; if (a.dscore_gain) off = align256(off + sizeof(float) * nb * s.J);
+  L.part_if = off; if (a.dif_gain) off = align256(off + sizeof(float) * nb);
   L.part_se = off; if (a.dscale_embed) off = align256(off + sizeof(float) * nb * s.J * s.D);
   L.se_slices = 0; L.se_per = 0;
   if (nb > 0) {
@@ -102,7 +101,7 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   p->qs = to_strides(a->q_stride); p->ks = to_strides(a->k_stride);
   p->vs = to_strides(a->v_stride); p->dos = to_strides(a->dout_stride);
   bwd_plan(*p, s.D, s.dtype, a->dscale_embed != nullptr);
-  if ((long long)s.B * s.H * p->n_chunks * p->wg_parts > INT_MAX / 2) return DSQG_EINVAL;
+  if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;
   if ((long long)s.B * s.H * p->n_tiles_kv > INT_MAX / 2) return DSQG_EINVAL;
   return DSQG_OK;
 }
@@ -212,7 +211,6 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
     ReduceParams r;
     r.B = s.B; r.H = s.H; r.J = s.J; r.D = s.D;
     r.n_chunks = rows ? p.n_chunks : 0;  // no rows: the empty sums write zeros
-    r.n_parts = r.n_chunks * p.wg_parts;
     r.part_bias = p.part_bias; r.part_se = p.part_se;
     r.part_gain = p.part_gain; r.part_if = p.part_if;
     r.dpos_bias = a->dpos_bias; r.dscale_embed = a->dscale_embed;

@@ -21,13 +21,13 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
   const int lane = threadIdx.x & 63;
   int t = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   const int JH = r.J * r.H;
-  const int per_h = r.B * r.n_parts;  // partial rows per head, ordered (b, row)
+  const int per_h = r.B * r.n_chunks;  // partials per head, ordered (b, chunk)
   if (t < JH) {  // dpos_bias[j,h]
     const int j = t / r.H, h = t - j * r.H;
     float s = 0.f;
     for (int k = lane; k < per_h; k += 64) {
-      const int bb = k / r.n_parts, c = k - bb * r.n_parts;
-      s += r.part_bias[((long long)(bb * r.H + h) * r.n_parts + c) * r.J + j];
+      const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
+      s += r.part_bias[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
     }
     s = wave_sum_fixed(s);
     if (lane == 0) r.dpos_bias[t] = s;
@@ -39,8 +39,8 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
       const int h = t / r.J, j = t - h * r.J;
       float s = 0.f;
       for (int k = lane; k < per_h; k += 64) {
-        const int bb = k / r.n_parts, c = k - bb * r.n_parts;
-        s += r.part_gain[((long long)(bb * r.H + h) * r.n_parts + c) * r.J + j];
+        const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
+        s += r.part_gain[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
       }
       s = wave_sum_fixed(s);
       if (lane == 0) r.dscore_gain[t] = s;
@@ -52,8 +52,8 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
     if (t < r.H) {
       float s = 0.f;
       for (int k = lane; k < per_h; k += 64) {
-        const int bb = k / r.n_parts, c = k - bb * r.n_parts;
-        s += r.part_if[(long long)(bb * r.H + t) * r.n_parts + c];
+        const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
+        s += r.part_if[(long long)(bb * r.H + t) * r.n_chunks + c];
       }
       s = wave_sum_fixed(s);
       if (lane == 0) r.dif_gain[t] = s;
@@ -114,7 +114,6 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
   if (tpb > p.n_tiles) tpb = p.n_tiles > 0 ? p.n_tiles : 1;
   p.tiles_per_block = tpb;
   p.n_chunks = p.n_tiles > 0 ? (p.n_tiles + tpb - 1) / tpb : 0;
-  p.wg_parts = mfma ? kBlock / 64 : 1;  // the MFMA dq kernel sums each wave's rows on its own
 }
 
 hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st) {

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
   constexpr int QT = 64;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
-  constexpr int RV = D + 16;              // LDS row stride for transposing reads
+  constexpr int RV = D + 8;               // LDS row stride (36 dwords at D=64: conflict-free 16-byte row reads)
   constexpr int WIN = QT + kMaxWindow;
   constexpr int CPR = D / 8;
   constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
     }
 
     // dbias / dg column sums of this wave's 16 table rows (its own writes, complete above),
-    // and the wave's sum of D' (for da): one partial row per wave, no workgroup barrier.
+    // and the wave's sum of D' (for da): no workgroup barrier inside the tile.
     if (l < J) {
       float sb = 0.f, sg = 0.f;
 #pragma unroll
@@ -433,12 +433,31 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
     }
   }
 
-  const long long prow = (long long)lb * (kBlock / 64) + w;  // this wave's partial row
-  if (l < J) {
-    p.part_bias[prow * J + l] = acc_bias;
-    if (g_grad) p.part_gain[prow * J + l] = acc_gain;
+  // The four waves' partial sums meet in their own (now free) table blocks; one partial row per
+  // workgroup, summed in wave order.
+  {
+    if constexpr (HAS_SE) __syncthreads();  // the last tile's dse reads of every wave's table are done
+    float* red = sDSw;  // wave-private until the barrier
+    if (l < J) { red[l] = acc_bias; red[64 + l] = acc_gain; }
+    if (l == 0) red[128] = acc_if;
+    __syncthreads();
+    if (tid < J) {
+      float sb = 0.f, sg = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        sb += sDS[ww * 16 * TS + tid];
+        sg += sDS[ww * 16 * TS + 64 + tid];
+      }
+      p.part_bias[(long long)lb * J + tid] = sb;
+      if (g_grad) p.part_gain[(long long)lb * J + tid] = sg;
+    }
+    if (tid == 0 && p.part_if) {
+      float sa = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) sa += sDS[ww * 16 * TS + 128];
+      p.part_if[lb] = sa;
+    }
   }
-  if (l == 0 && p.part_if) p.part_if[prow] = acc_if;
   if constexpr (HAS_SE) {
     if (se_grad) {
       // Lane (i, g) of tile (jb, db) holds dSE^T[d = 16 db + 4 g + r][j = 16 jb + i], r = 0..3.

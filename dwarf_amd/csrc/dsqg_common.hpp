@@ -137,7 +137,6 @@ struct BwdParams {
   int n_tiles;          // query tiles per (b,h) of the dq launch
   int tiles_per_block;  // consecutive tiles of one (b,h) handled by one dq workgroup
   int n_chunks;         // dq workgroups per (b,h)
-  int wg_parts;         // dbias / dg / da partial rows per dq workgroup (one per wave: 4)
   int n_tiles_kv;       // key tiles per (b,h) of the dk/dv launch (one workgroup each)
   float scale;
   TapTable taps;
@@ -154,15 +153,14 @@ struct BwdParams {
   void* dk; Strides4 dks;
   void* dv; Strides4 dvs;
   float* dpre;        // workspace [B,H,N]: D' = dOut . o (pre-gain o), fp32
-  float* part_bias;   // workspace [B*H*n_chunks*wg_parts][J]
+  float* part_bias;   // workspace [B*H*n_chunks][J]
   float* part_se;     // workspace [B*H*n_chunks][J][D] or null
-  float* part_gain;   // workspace [B*H*n_chunks*wg_parts][J] or null
-  float* part_if;     // workspace [B*H*n_chunks*wg_parts] or null
+  float* part_gain;   // workspace [B*H*n_chunks][J] or null
+  float* part_if;     // workspace [B*H*n_chunks] or null
 };
 
 struct ReduceParams {
   int B, H, J, D, n_chunks;
-  int n_parts;  // dbias / dg / da partial rows per (b,h): n_chunks * wg_parts, ordered (b, row)
   const float* part_bias; const float* part_se; const float* part_gain; const float* part_if;
   float* dpos_bias; float* dscale_embed; float* dscore_gain; float* dif_gain;
   // dscale_embed is summed in two stages: se_slices runs of se_per consecutive workgroup
