@@ -199,25 +199,33 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
 
   hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   const bool rows = (long long)s.B * s.H * s.N > 0;
+  ReduceParams r;
+  memset(&r, 0, sizeof(r));
+  r.B = s.B; r.H = s.H; r.J = s.J; r.D = s.D;
+  r.n_chunks = rows ? p.n_chunks : 0;  // no rows: the empty sums write zeros
+  r.part_bias = p.part_bias; r.part_se = p.part_se;
+  r.part_gain = p.part_gain; r.part_if = p.part_if;
+  r.dpos_bias = a->dpos_bias; r.dscale_embed = a->dscale_embed;
+  r.dscore_gain = a->dscore_gain; r.dif_gain = a->dif_gain;
+  r.se_stage = a->dscale_embed ? reinterpret_cast<float*>(ws + L.se_stage) : nullptr;
+  r.se_slices = rows ? L.se_slices : 0;
+  r.se_per = L.se_per;
+  const unsigned nb_dq = (unsigned)((long long)s.B * s.H * p.n_chunks);
+  const unsigned nb_kv = (unsigned)((long long)s.B * s.H * p.n_tiles_kv);
+  if (phases == kPhaseAll && rows) {
+    // dq (with the partials), dscale_embed's first stage, then dk/dv with the rest of the
+    // parameter reduction in the same launch.
+    if ((st = hip_status(launch_bwd_dq(p, s.dtype, s.D, nb_dq, hs)))) return st;
+    if ((st = hip_status(launch_bwd_reduce_se_stage(r, hs)))) return st;
+    return hip_status(launch_bwd_dkdv_params(p, r, s.dtype, s.D, nb_kv, hs));
+  }
   if ((phases & kPhaseDq) && rows) {
-    const unsigned nb = (unsigned)((long long)s.B * s.H * p.n_chunks);
-    if ((st = hip_status(launch_bwd_dq(p, s.dtype, s.D, nb, hs)))) return st;
+    if ((st = hip_status(launch_bwd_dq(p, s.dtype, s.D, nb_dq, hs)))) return st;
   }
   if ((phases & kPhaseDkdv) && rows) {
-    const unsigned nb = (unsigned)((long long)s.B * s.H * p.n_tiles_kv);
-    if ((st = hip_status(launch_bwd_dkdv(p, s.dtype, s.D, nb, hs)))) return st;
+    if ((st = hip_status(launch_bwd_dkdv(p, s.dtype, s.D, nb_kv, hs)))) return st;
   }
   if (phases & kPhaseParams) {
-    ReduceParams r;
-    r.B = s.B; r.H = s.H; r.J = s.J; r.D = s.D;
-    r.n_chunks = rows ? p.n_chunks : 0;  // no rows: the empty sums write zeros
-    r.part_bias = p.part_bias; r.part_se = p.part_se;
-    r.part_gain = p.part_gain; r.part_if = p.part_if;
-    r.dpos_bias = a->dpos_bias; r.dscale_embed = a->dscale_embed;
-    r.dscore_gain = a->dscore_gain; r.dif_gain = a->dif_gain;
-    r.se_stage = a->dscale_embed ? reinterpret_cast<float*>(ws + L.se_stage) : nullptr;
-    r.se_slices = rows ? L.se_slices : 0;
-    r.se_per = L.se_per;
     if ((st = hip_status(launch_bwd_reduce(r, hs)))) return st;
   }
   return DSQG_OK;

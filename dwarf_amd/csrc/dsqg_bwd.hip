@@ -6,68 +6,12 @@
 // (kernels/dsqg_attention_v3.py:265-271), whose summation order varies run to run.
 #include "dsqg_common.hpp"
 #include "dsqg_launch.hpp"
+#include "dsqg_reduce.hpp"
 
 namespace dsqg {
 
-// One wave per parameter-gradient element: lane l sums partials l, l+64, ... in order, then a
-// fixed xor-tree combines the lanes, so the result is the same on every run.
-__device__ __forceinline__ float wave_sum_fixed(float x) {
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) x += __shfl_xor(x, s, 64);
-  return x;
-}
-
 __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
-  const int lane = threadIdx.x & 63;
-  int t = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
-  const int JH = r.J * r.H;
-  const int per_h = r.B * r.n_chunks;  // partials per head, ordered (b, chunk)
-  if (t < JH) {  // dpos_bias[j,h]
-    const int j = t / r.H, h = t - j * r.H;
-    float s = 0.f;
-    for (int k = lane; k < per_h; k += 64) {
-      const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
-      s += r.part_bias[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
-    }
-    s = wave_sum_fixed(s);
-    if (lane == 0) r.dpos_bias[t] = s;
-    return;
-  }
-  t -= JH;
-  if (r.dscore_gain) {
-    if (t < JH) {  // dscore_gain[h,j]
-      const int h = t / r.J, j = t - h * r.J;
-      float s = 0.f;
-      for (int k = lane; k < per_h; k += 64) {
-        const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
-        s += r.part_gain[((long long)(bb * r.H + h) * r.n_chunks + c) * r.J + j];
-      }
-      s = wave_sum_fixed(s);
-      if (lane == 0) r.dscore_gain[t] = s;
-      return;
-    }
-    t -= JH;
-  }
-  if (r.dif_gain) {
-    if (t < r.H) {
-      float s = 0.f;
-      for (int k = lane; k < per_h; k += 64) {
-        const int bb = k / r.n_chunks, c = k - bb * r.n_chunks;
-        s += r.part_if[(long long)(bb * r.H + t) * r.n_chunks + c];
-      }
-      s = wave_sum_fixed(s);
-      if (lane == 0) r.dif_gain[t] = s;
-      return;
-    }
-    t -= r.H;
-  }
-  if (r.dscale_embed && t < r.J * r.D) {
-    const long long stride = (long long)r.J * r.D;
-    float s = 0.f;
-    for (int k = lane; k < r.se_slices; k += 64) s += r.se_stage[k * stride + t];
-    s = wave_sum_fixed(s);
-    if (lane == 0) r.dscale_embed[t] = s;
-  }
+  reduce_params_wave(r, blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6), threadIdx.x & 63);
 }
 
 // First stage of the dscale_embed sum: workgroup (x, y) sums, for 256 consecutive elements of
@@ -116,15 +60,24 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
   p.n_chunks = p.n_tiles > 0 ? (p.n_tiles + tpb - 1) / tpb : 0;
 }
 
-hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st) {
+hipError_t launch_bwd_reduce_se_stage(const ReduceParams& r, hipStream_t st) {
   if (r.dscale_embed && r.se_slices > 0) {
     const long long JD = (long long)r.J * r.D;
     hipLaunchKernelGGL(bwd_reduce_se_stage_kernel, dim3((unsigned)((JD + kBlock - 1) / kBlock), (unsigned)r.se_slices),
                        dim3(kBlock), 0, st, r);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    return hipGetLastError();
   }
-  const long long total = 2LL * r.J * r.H + r.H + (long long)r.J * r.D;  // outputs (upper bound)
+  return hipSuccess;
+}
+
+hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st) {
+  const hipError_t e = launch_bwd_reduce_se_stage(r, st);
+  if (e != hipSuccess) return e;
+  return launch_bwd_reduce_final(r, st);
+}
+
+hipError_t launch_bwd_reduce_final(const ReduceParams& r, hipStream_t st) {
+  const long long total = reduce_params_waves(r);
   if (total == 0) return hipSuccess;
   const long long waves_per_block = kBlock / 64;
   hipLaunchKernelGGL(bwd_reduce_kernel, dim3((unsigned)((total + waves_per_block - 1) / waves_per_block)),

@@ -8,6 +8,7 @@
 // Follows _bwd_dkdv_v3 (kernels/dsqg_attention_v3.py:282-352), which also needs no atomics.
 #include "dsqg_common.hpp"
 #include "dsqg_launch.hpp"
+#include "dsqg_reduce.hpp"
 
 namespace dsqg {
 
@@ -151,6 +152,18 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, unsigned nblock
   if (bwd_mfma_supported(p, D, dtype)) return launch_bwd_dkdv_mfma(p, D, nblocks, st);
   return dtype == 0 ? launch_bwd_dkdv_dtype<float>(p, D, nblocks, st)
                     : launch_bwd_dkdv_dtype<bf16_t>(p, D, nblocks, st);
+}
+
+hipError_t launch_bwd_dkdv_params(const BwdParams& p, const ReduceParams& r, int dtype, int D,
+                                  unsigned nblocks, hipStream_t st) {
+  if (bwd_mfma_supported(p, D, dtype)) {
+    BwdParams pr = p;
+    pr.red = r;
+    pr.red_blocks = (int)((reduce_params_waves(r) + kBlock / 64 - 1) / (kBlock / 64));
+    return launch_bwd_dkdv_mfma(pr, D, nblocks + (unsigned)pr.red_blocks, st);
+  }
+  const hipError_t e = launch_bwd_dkdv(p, dtype, D, nblocks, st);
+  return e != hipSuccess ? e : launch_bwd_reduce_final(r, st);
 }
 
 }  // namespace dsqg

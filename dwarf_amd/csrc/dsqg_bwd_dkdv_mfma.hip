@@ -17,10 +17,13 @@
 //    are staged in a wave-private LDS block for the transposed reads of the diagonal update.
 //  * The q.se_j term of the score (scale_embed) is a [query][tap] table per wave computed on the
 //    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps.
+// With p.red_blocks > 0 the launch carries that many extra workgroups at the end of the grid,
+// which sum the parameter-gradient partials (dsqg_reduce.hpp) while the dk/dv tiles run.
 // Follows _bwd_dkdv_v3 (kernels/dsqg_attention_v3.py:282-352).
 #include "dsqg_common.hpp"
 #include "dsqg_launch.hpp"
 #include "dsqg_mfma.hpp"
+#include "dsqg_reduce.hpp"
 
 namespace dsqg {
 
@@ -56,7 +59,13 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel
   __shared__ float2 sPair[4][16];                    // per wave: long-range (score, dOut.v) of one tap
 
   const int tid = threadIdx.x;
-  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  // Workgroups past the dk/dv tiles run the parameter reduction (partials from launch 1).
+  const int kv_blocks = (int)gridDim.x - p.red_blocks;
+  if ((int)blockIdx.x >= kv_blocks) {
+    reduce_params_wave(p.red, ((int)blockIdx.x - kv_blocks) * (kBlock / 64) + (tid >> 6), tid & 63);
+    return;
+  }
+  const int lb = xcd_logical_block(blockIdx.x, kv_blocks);
   const int bh = lb / p.n_tiles_kv, tile = lb - bh * p.n_tiles_kv;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;

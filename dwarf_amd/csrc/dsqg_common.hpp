@@ -132,6 +132,15 @@ struct FwdParams {
   float* lse;                // [B,H,N] or null
 };
 
+struct ReduceParams {
+  int B, H, J, D, n_chunks;
+  const float* part_bias; const float* part_se; const float* part_gain; const float* part_if;
+  float* dpos_bias; float* dscale_embed; float* dscore_gain; float* dif_gain;
+  // dscale_embed is summed in two stages: se_slices runs of se_per consecutive workgroup
+  // partials each, summed column-wise into se_stage [se_slices][J*D], then the slices.
+  float* se_stage; int se_slices, se_per;
+};
+
 struct BwdParams {
   int B, H, N;
   int n_tiles;          // query tiles per (b,h) of the dq launch
@@ -157,16 +166,11 @@ struct BwdParams {
   float* part_se;     // workspace [B*H*n_chunks][J][D] or null
   float* part_gain;   // workspace [B*H*n_chunks][J] or null
   float* part_if;     // workspace [B*H*n_chunks] or null
+  // Parameter reduction run by red_blocks extra workgroups of the bf16 dk/dv launch (0: none).
+  ReduceParams red;
+  int red_blocks;
 };
 
-struct ReduceParams {
-  int B, H, J, D, n_chunks;
-  const float* part_bias; const float* part_se; const float* part_gain; const float* part_if;
-  float* dpos_bias; float* dscale_embed; float* dscore_gain; float* dif_gain;
-  // dscale_embed is summed in two stages: se_slices runs of se_per consecutive workgroup
-  // partials each, summed column-wise into se_stage [se_slices][J*D], then the slices.
-  float* se_stage; int se_slices, se_per;
-};
 
 struct DecodeParams {
   int B, H, S;

@@ -25,6 +25,14 @@ bool bwd_mfma_supported(const BwdParams& p, int D, int dtype);
 hipError_t launch_bwd_dq_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_dkdv_mfma(const BwdParams& p, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_reduce(const ReduceParams& r, hipStream_t st);
+// dscale_embed's first reduction stage alone (a no-op without dscale_embed), and the rest.
+hipError_t launch_bwd_reduce_se_stage(const ReduceParams& r, hipStream_t st);
+hipError_t launch_bwd_reduce_final(const ReduceParams& r, hipStream_t st);
+// dk/dv and then the parameter reduction r: with the bf16 MFMA dk/dv kernel the reduction
+// rides in the same launch as extra workgroups; otherwise two launches.  r's dscale_embed
+// first stage must already have run.
+hipError_t launch_bwd_dkdv_params(const BwdParams& p, const ReduceParams& r, int dtype, int D,
+                                  unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st);
 
