@@ -154,7 +154,7 @@ def bench_decode(dev, steps=1000):
             "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "timing": "hipGraph replay, HIP events"}
 
 
-def bench_module(dev, steps=20, warmup=5):
+def bench_module(dev, steps=20, warmup=20):
     """DSQGAttentionQW (E768 H12, the config-2 attention layer) fwd+bwd in bf16 on x [8,2048,768]:
     as shipped (q, k, v strided views of the qkv projection) and with the reference's
     permute().contiguous() copies put back (train/train_2048_condU.py:173-175)."""
@@ -244,8 +244,9 @@ def profile_mode(args, w, dev):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=200,
+                    help="untimed steps first (the GPU clocks ramp during the first ~20 ms of work)")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3])
     ap.add_argument("--sets", type=int, default=3, help="input sets rotated between steps")
     ap.add_argument("--decode-steps", type=int, default=1000)
@@ -311,21 +312,35 @@ def main(argv=None):
     torch.cuda.synchronize()
     print(f"[bench] fwd+bwd {ms:.4f} ms/step (wall {wall:.4f})", file=sys.stderr, flush=True)
 
-    # Per-kernel launch durations (each phase launched back to back, rotating the sets).
-    kern = {
-        "dsqg_fwd": (lambda i: sets[i % len(sets)][2].run(), w.fwd_bytes()),
-        "dsqg_bwd_dq": (lambda i: sets[i % len(sets)][3].run("dq"), 5 * T * w.D * E + 8 * T),
-        "dsqg_bwd_dkdv": (lambda i: sets[i % len(sets)][3].run("dkdv"), 6 * T * w.D * E + 8 * T),
-        "dsqg_bwd_params": (lambda i: sets[i % len(sets)][3].run("params"), None),
-    }
+    # Per-kernel launch durations inside the step's own order (fwd, dq, dk/dv, params; rotating
+    # the sets), so every kernel meets the caches the step leaves it: a HIP event after each
+    # launch, median over the steps.  (A full backward runs the parameter reduction inside the
+    # dk/dv launch; here the phases are launched one by one.)
+    names = ("dsqg_fwd", "dsqg_bwd_dq", "dsqg_bwd_dkdv", "dsqg_bwd_params")
+    nbytes_of = {"dsqg_fwd": w.fwd_bytes(), "dsqg_bwd_dq": 5 * T * w.D * E + 8 * T,
+                 "dsqg_bwd_dkdv": 6 * T * w.D * E + 8 * T, "dsqg_bwd_params": None}
+    reps = args.steps
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(reps)]
+    torch.cuda.synchronize()
+    for i in range(reps):
+        _, _, fl, bl = sets[i % len(sets)]
+        ev[i][0].record(stream)
+        fl.run()
+        ev[i][1].record(stream)
+        bl.run("dq")
+        ev[i][2].record(stream)
+        bl.run("dkdv")
+        ev[i][3].record(stream)
+        bl.run("params")
+        ev[i][4].record(stream)
+    torch.cuda.synchronize()
     per = {}
-    for name, (fn, nbytes) in kern.items():
-        fn(0)
-        us = _events_ms(fn, args.steps, stream) * 1000.0
+    for k, name in enumerate(names):
+        us = statistics.median(ev[i][k].elapsed_time(ev[i][k + 1]) for i in range(reps)) * 1000.0
         per[name] = {"us": round(us, 3)}
-        if nbytes:
-            per[name]["algorithmic_bytes"] = nbytes
-            per[name]["achieved_GBs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+        if nbytes_of[name]:
+            per[name]["algorithmic_bytes"] = nbytes_of[name]
+            per[name]["achieved_GBs"] = round(nbytes_of[name] / (us * 1e-6) / 1e9, 1)
         print(f"[bench] {name}: {us:.2f} us/launch", file=sys.stderr, flush=True)
     dom = max((k for k in per if "algorithmic_bytes" in per[k]), key=lambda k: per[k]["us"])
     achieved = per[dom]["achieved_GBs"]
