@@ -14,7 +14,8 @@
 //    vector L1 serves that at close to four times the rate of the MFMA operand order); q.k,
 //    dOut.v and q.se_j are VALU dot products (v_dot2_f32_bf16, DPP sums over the row's lanes)
 //    handed to the diagonal lane (16*(i/4)+i, register i%4) through LDS.  The query / dOut rows
-//    are staged in a wave-private LDS block for the transposed reads of the diagonal update.
+//    are staged in the wave's rows of the (by then free) window tiles for the transposed reads
+//    of the diagonal update; the LDS then fits four workgroups per CU (three with scale_embed).
 //  * The q.se_j term of the score (scale_embed) is a [query][tap] table per wave computed on the
 //    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps.
 // With p.red_blocks > 0 the launch carries that many extra workgroups at the end of the grid,
@@ -28,11 +29,11 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_dkdv_mfma_kernel(BwdParams p) {
   constexpr int KT = 64;                  // key rows per workgroup
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
-  constexpr int RV = D + 16;
+  constexpr int RV = D + 8;               // LDS row stride (36 dwords at D=64)
   constexpr int WIN = KT + kMaxWindow;    // query window rows [m0, m0+96)
   constexpr int CPR = D / 8;
   constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
@@ -47,10 +48,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel
 
   __shared__ __align__(16) bf16_t sQ[WIN * RV];
   __shared__ __align__(16) bf16_t sO[WIN * RV];
-  // Wave-private long-range query / dOut rows.  With scale_embed they reuse the window tiles
-  // once the band is done (the LDS then fits three workgroups per CU).
-  __shared__ __align__(16) bf16_t sQs[HAS_SE ? 8 : 4 * 16 * RV];
-  __shared__ __align__(16) bf16_t sOs[HAS_SE ? 8 : 4 * 16 * RV];
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
   __shared__ float sT[HAS_SE ? WIN * TS : 1];        // log2e (bias + c q.se), window query x dense tap
   __shared__ float sBias2[kMaxTaps];
@@ -129,31 +126,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel
       dq_[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
     }
   // lse and D' of the query on this lane's diagonal for the long-range taps (query m + delta;
-  // lanes off the diagonal fetch a harmless value): all of them before the tap loop, or with
-  // scale_embed (fewer free registers) in a ring LPF taps ahead, like the query rows.
-  constexpr int LPF = HAS_SE ? PF : NSM;
+  // lanes off the diagonal fetch a harmless value), in a ring PF taps ahead like the query rows.
+  constexpr int LPF = PF;
   float lseS[LPF], dpS[LPF];
   auto load_lse = [&](int t) {
     const int nq = m + p.taps.delta[W + 1 + t];
     lseS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
     dpS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
   };
-#pragma unroll
-  for (int t = 0; t < LPF; ++t)
-    if (NSC > 0 ? t < NSC : t < NS) load_lse(t);
-  // Long-range query / dOut rows m0w + delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
-  uint4 qS[PF][CHW], oS[PF][CHW];
-#pragma unroll
-  for (int t = 0; t < PF; ++t) {
-    if (t < NS) {
-      const int n0 = m0w + p.taps.delta[W + 1 + t];
-#pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        qS[t][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
-        oS[t][u] = bload16(rO, n0 * dosn + olaneR[u]);
-      }
-    }
-  }
 
   for (int j = tid; j < J; j += kBlock) {
     const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
@@ -246,10 +226,30 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel
   }
 
   // ---- Long-range taps: queries m0w + delta + 0..15, diagonal of one tile each. ----
+  // Their first loads are issued only now: during the band the registers hold the band's
+  // operands, and four workgroups per CU cover the wait.
+#pragma unroll
+  for (int t = 0; t < LPF; ++t)
+    if (NSC > 0 ? t < NSC : t < NS) load_lse(t);
+  // Long-range query / dOut rows m0w + delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
+  uint4 qS[PF][CHW], oS[PF][CHW];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) {
+    if (t < NS) {
+      const int n0 = m0w + p.taps.delta[W + 1 + t];
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        qS[t][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
+        oS[t][u] = bload16(rO, n0 * dosn + olaneR[u]);
+      }
+    }
+  }
   const bool diag = g == (i >> 2);
-  bf16_t* qsw = (HAS_SE ? sQ : sQs) + w * 16 * RV;
-  bf16_t* osw = (HAS_SE ? sO : sOs) + w * 16 * RV;
-  if constexpr (HAS_SE) __syncthreads();  // every wave's band reads of sQ / sO are done
+  // The wave's long-range query / dOut rows are staged in the window tiles (rows 16w..16w+15),
+  // free once every wave's band is done.
+  bf16_t* qsw = sQ + w * 16 * RV;
+  bf16_t* osw = sO + w * 16 * RV;
+  __syncthreads();  // every wave's band reads of sQ / sO are done
   const bf16_t* qtr = qsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
   const bf16_t* otr = osw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void bwd_dkdv_mfma_kernel
         if (rc_chunk<D>(l, u) == 0) sPair[w][rc_row<D>(l, u)] = float2{dk, dv};
       }
       if (t + PF < NS) {
-        if constexpr (HAS_SE) load_lse(t + PF);
+        load_lse(t + PF);
         const int n0 = m0w + p.taps.delta[W + 1 + t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
