@@ -295,3 +295,30 @@ def test_qkv_entry_matches_split_heads(gpu_device, dtype):
         assert torch.equal(x, y), name
     # The head merge of the output is a view: [B,H,N,D] stored token-major.
     assert res[0][0].permute(0, 2, 1, 3).is_contiguous()
+
+
+@pytest.mark.parametrize("dtype,D,se", [(torch.bfloat16, 64, False), (torch.bfloat16, 64, True),
+                                         (torch.bfloat16, 32, True), (torch.float32, 64, True)])
+def test_phase_by_phase_backward_equals_full(gpu_device, dtype, D, se):
+    """dsqg_bwd_dq + dsqg_bwd_dkdv + dsqg_bwd_params give bit for bit what dsqg_bwd gives (the
+    full backward runs the parameter reduction inside the dk/dv launch)."""
+    inp = _rand_inputs(2, 3, 700, D, OFFSETS_V3, dtype, seed=31, se=se)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d.get("scale_embed"),
+                       d.get("score_gain"), d.get("if_gain"), list(OFFSETS_V3))
+    fl.run()
+    res = []
+    for phased in (False, True):
+        bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
+                           d.get("scale_embed"), d.get("score_gain"), d.get("if_gain"),
+                           list(OFFSETS_V3), se, True, True)
+        if phased:
+            for phase in ("dq", "dkdv", "params"):
+                bl.run(phase)
+        else:
+            bl.run()
+        torch.cuda.synchronize(gpu_device)
+        res.append([t.clone() for t in bl.outputs()])
+    for name, x, y in zip(("dq", "dk", "dv", "dpos_bias", "dscale_embed", "dscore_gain",
+                           "dif_gain"), *res):
+        assert torch.equal(x, y), name
