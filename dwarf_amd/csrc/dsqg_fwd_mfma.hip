@@ -33,11 +33,11 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void fwd_mfma_kernel(FwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4)) void fwd_mfma_kernel(FwdParams p) {
   constexpr int QT = 64;                  // query rows per workgroup
   constexpr int KS = D / 32;              // 16x16x32 steps over the head dim
   constexpr int DB = D / 16;              // 16-wide head-dim blocks of the output
-  constexpr int RV = D + 16;              // LDS row stride of V tiles (transposing reads)
+  constexpr int RV = D + 8;               // LDS row stride of the K / V tiles (36 dwords at D=64)
   constexpr int WIN = QT + kMaxWindow;    // dense-window rows of V staged in LDS
   constexpr int CPR = D / 8;              // 16-byte chunks per row
   constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
@@ -47,11 +47,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void fwd_mfma_kernel(FwdP
   constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
   constexpr int TS = 38;                  // row stride of the per-wave T table (dense taps; 2-way reads)
   constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
+  constexpr int XE = 8 * 2 * (D + 4);     // bf16 elements of the output exchange (8 rows x (D+4) floats)
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sV[WIN * RV];
   __shared__ __align__(16) bf16_t sK[WIN * RV];   // dense-window K rows (MFMA A operands)
-  __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : 16 * RV];   // wave-private staging block
+  __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : XE];   // wave-private staging block
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
   __shared__ __align__(16) float sRaw[4][16 * 16];   // per wave: long-range q.k [query][tap]
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
@@ -309,6 +310,13 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : 3) void fwd_mfma_kernel(FwdP
 #pragma unroll
         for (int u = 0; u < CHW; ++u) vS[t % PF][u] = bload16(rV, r0 * vsn + vlane[u]);
       }
+      // Pin this tap's multiply-adds here: left free, the compiler defers every tap's
+      // accumulation behind all the loads and spills (14 registers at four workgroups per CU).
+#pragma unroll
+      for (int u = 0; u < CHW; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(oL[u][e]));
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
