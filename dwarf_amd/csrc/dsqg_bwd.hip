@@ -49,11 +49,11 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
   p.n_tiles = (p.N + QPB - 1) / QPB;
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
   const long long work = (long long)p.B * p.H * p.n_tiles;
-  // Several tiles per workgroup only to bound the [J, D] dscale_embed partials; the dbias / dg /
-  // da partial rows are small next to a tile's loads, so otherwise one tile per workgroup (the
-  // MFMA kernel's single-tile form then keeps no per-lane addresses across tiles).
-  const long long target = se_grad ? 2048 : work;
-  int tpb = (int)((work + target - 1) / (target > 0 ? target : 1));
+  // One tile per workgroup: the partial rows (J floats, and J x D for dscale_embed) are small next
+  // to a tile's loads, and the MFMA kernels' single-tile form keeps no per-lane addresses across
+  // tiles (a tile loop costs them a third of their registers).
+  (void)se_grad;
+  int tpb = 1;
   if (tpb < 1) tpb = 1;
   if (tpb > p.n_tiles) tpb = p.n_tiles > 0 ? p.n_tiles : 1;
   p.tiles_per_block = tpb;

@@ -32,7 +32,7 @@ namespace dsqg {
 constexpr int kDqTableStride = 48;
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int QT = 64;
   constexpr int KS = D / 32;
   constexpr int DB = D / 16;
@@ -58,7 +58,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
   // (read by every wave for dse).
   __shared__ __align__(16) bf16_t sKs[4][HAS_SE ? KSB : 16 * RV];
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];     // scale_embed rows, bf16
-  __shared__ __align__(16) float sDS[4 * 16 * TS];      // dS[query][tap] per wave
+  // dS[query][tap] per wave; with scale_embed it lives in the V window once the band is done
+  // (D >= 64), which leaves room for three workgroups per CU.
+  constexpr bool TBL_IN_V = HAS_SE && WIN * RV * 2 >= 4 * 16 * TS * 4;
+  __shared__ __align__(16) float sDSst[TBL_IN_V ? 4 : 4 * 16 * TS];
   // c q.k per (query, tap), for dg only: dynamic LDS, present when score_gain's gradient is
   // requested (without it the workgroup fits three per CU).
   extern __shared__ __align__(16) float sDyn[];
@@ -112,10 +115,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
     }
   }
 
-  // Table columns J..47 are read as zeros (whole 4-wide groups feed the MFMA operands).
+  float* const sDS = TBL_IN_V ? reinterpret_cast<float*>(sV) : sDSst;
+  // Table columns J..47 are read as zeros (whole 4-wide groups feed the MFMA operands); a table
+  // in the V window gets them after the band.
   for (int e = tid; e < 4 * 16 * (48 - J); e += kBlock) {
     const int row = e / (48 - J), j = J + e % (48 - J);
-    sDS[row * TS + j] = 0.f;
+    if (!TBL_IN_V) sDS[row * TS + j] = 0.f;
     if (g_grad) sRAW[row * TS + j] = 0.f;
   }
 
@@ -133,7 +138,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
   const int t_begin = chunk * p.tiles_per_block;
   // Without scale_embed the plan gives one tile per workgroup (checked at launch): a loop of
   // one trip keeps the compiler from holding loop-invariant addresses across tiles.
-  const int t_end = HAS_SE ? min(p.n_tiles, t_begin + p.tiles_per_block) : t_begin + 1;
+  const int t_end = t_begin + 1;
 
   for (int tile = t_begin; tile < t_end; ++tile) {
     const int n0 = tile * QT;
@@ -268,6 +273,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 2 : 3)) void bwd_d
       }
     }
 
+    if constexpr (TBL_IN_V) {
+      __syncthreads();  // every wave's band reads of sV are done: the dS tables move in
+      for (int e = l; e < 16 * (48 - J); e += 64) sDSw[(e / (48 - J)) * TS + J + e % (48 - J)] = 0.f;
+    }
     // ---- Long-range taps (diagonal of one 16x16 tile each). ----
     const bool diag = g == (i >> 2);
     float als[NSM], uus[NSM];
@@ -488,12 +497,9 @@ static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
 template <int D>
 static hipError_t launch_dq_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
   // The scale_embed variant also serves dse requested at se = 0.
-  if (p.scale_embed || p.part_se) {
-    launch_dq_mfma_ns<D, true>(p, nb, st);
-  } else {
-    if (p.tiles_per_block != 1) return hipErrorInvalidValue;  // the single-tile form
-    launch_dq_mfma_ns<D, false>(p, nb, st);
-  }
+  if (p.tiles_per_block != 1) return hipErrorInvalidValue;  // the single-tile form
+  if (p.scale_embed || p.part_se) launch_dq_mfma_ns<D, true>(p, nb, st);
+  else launch_dq_mfma_ns<D, false>(p, nb, st);
   return hipGetLastError();
 }
 
