@@ -84,10 +84,12 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   constexpr int E = sizeof(T);
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // The wave index is uniform: readfirstlane keeps (b, h), the row pointers and the ring's buffer
+  // resources in scalar registers (a resource in vector registers costs every load a loop).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const long long bh = (long long)blockIdx.x * (kBlock / 64) + wave;
   if (bh >= (long long)p.B * p.H) return;
-  const int b = (int)(bh / p.H), h = (int)(bh - (long long)b * p.H);
+  const int b = (int)bh / p.H, h = (int)bh - b * p.H;  // B * H < 2^31 (checked by the ABI)
   const int r = lane / G, g = lane - r * G;
   const int d0 = g * 8;
   const int J = p.taps.J, S = p.S;
