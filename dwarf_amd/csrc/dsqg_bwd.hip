@@ -11,7 +11,7 @@
 namespace dsqg {
 
 __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
-  reduce_params_wave(r, blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6), threadIdx.x & 63);
+  reduce_params_wave(r, blockIdx.x * (kBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
 }
 
 // First stage of the dscale_embed sum: workgroup (x, y) sums, for 256 consecutive elements of

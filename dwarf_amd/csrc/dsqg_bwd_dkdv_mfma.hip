@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
   // Workgroups past the dk/dv tiles run the parameter reduction (partials from launch 1).
   const int kv_blocks = (int)gridDim.x - p.red_blocks;
   if ((int)blockIdx.x >= kv_blocks) {
-    reduce_params_wave(p.red, ((int)blockIdx.x - kv_blocks) * (kBlock / 64) + (tid >> 6), tid & 63);
+    reduce_params_wave(p.red, ((int)blockIdx.x - kv_blocks) * (kBlock / 64) + __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63);
     return;
   }
   const int lb = xcd_logical_block(blockIdx.x, kv_blocks);
