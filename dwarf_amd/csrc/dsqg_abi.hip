@@ -33,6 +33,7 @@ int check_shape(const dsqg_shape& s, bool need_n, TapTable* taps) {
   while (W + 1 < s.J && W + 1 <= kMaxWindow && s.offsets[W + 1] == W + 1) ++W;
   taps->W = W;
   for (int j = 0; j < kMaxOffsets; ++j) taps->delta[j] = j < s.J ? s.offsets[j] : 0;
+  for (int t = 0; t < kMaxSparse; ++t) taps->sdelta[t] = W + 1 + t < s.J ? s.offsets[W + 1 + t] : 0;
   return DSQG_OK;
 }
 

@@ -84,6 +84,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
   const int m0w = m0 + 16 * w;
   const int m = m0w + i;                  // key row of this lane's MFMA column
   const bool key_ok = m < N;
+  int dl_s[NSM];
+  load_sparse_deltas(p.taps, dl_s);
   const int klane = opaque(i * ksn + 8 * g), vlane = opaque(i * vsn + 8 * g);
   // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
   int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
@@ -130,7 +132,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
   constexpr int LPF = PF;
   float lseS[LPF], dpS[LPF];
   auto load_lse = [&](int t) {
-    const int nq = m + p.taps.delta[W + 1 + t];
+    const int nq = m + dl_s[t];
     lseS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
     dpS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
   };
@@ -236,7 +238,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
     if (t < NS) {
-      const int n0 = m0w + p.taps.delta[W + 1 + t];
+      const int n0 = m0w + dl_s[t];
 #pragma unroll
       for (int u = 0; u < CHW; ++u) {
         qS[t][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      const int dl = p.taps.delta[j];
+      const int dl = dl_s[t];
       // This tap's lse / D' (taken before the ring slot is refilled for tap t + PF).
       const float lseq = lseS[t % LPF], dpq = dpS[t % LPF];
       // The score's dot products (gain c log2e q.k + c log2e q.se_j) and dOut.v on the VALU:
@@ -278,7 +280,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
       }
       if (t + PF < NS) {
         load_lse(t + PF);
-        const int n0 = m0w + p.taps.delta[W + 1 + t + PF];
+        const int n0 = m0w + dl_s[t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
           qS[t % PF][u] = bload16(rQ, n0 * qsn + qlaneR[u]);

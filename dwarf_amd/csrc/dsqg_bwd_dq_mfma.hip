@@ -139,6 +139,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
   // Without scale_embed the plan gives one tile per workgroup (checked at launch): a loop of
   // one trip keeps the compiler from holding loop-invariant addresses across tiles.
   const int t_end = t_begin + 1;
+  int dl_s[NSM];
+  load_sparse_deltas(p.taps, dl_s);
 
   for (int tile = t_begin; tile < t_end; ++tile) {
     const int n0 = tile * QT;
@@ -173,7 +175,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
 #pragma unroll
     for (int t = 0; t < PF; ++t) {
       if (t < NS) {
-        const int m0 = n0w - p.taps.delta[W + 1 + t];
+        const int m0 = n0w - dl_s[t];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
           kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
           }
         }
         if (t + PF < NS) {
-          const int m0 = n0w - p.taps.delta[W + 1 + t + PF];
+          const int m0 = n0w - dl_s[t + PF];
 #pragma unroll
           for (int u = 0; u < CHW; ++u) {
             kS[t % PF][u] = bload16(rK, m0 * ksn + klaneR[u]);
@@ -326,7 +328,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
           const float2 pr = *reinterpret_cast<const float2*>(sPair[w][i]);
           raw = pr.x; uval = pr.y; s2 = fmaf(sGain[j] * c2, raw, sBias2[j]);
         }
-        const bool ok = diag && row_ok && n >= p.taps.delta[j];
+        const bool ok = diag && row_ok && n >= dl_s[t];
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         als[t] = alpha;
         uus[t] = uval;

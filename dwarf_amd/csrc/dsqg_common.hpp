@@ -114,6 +114,9 @@ struct TapTable {
   int W;        // dense window: offsets[j] == j for j <= W (W <= kMaxWindow)
   int maxd;     // largest offset
   int delta[kMaxOffsets];
+  // Offsets of the long-range taps (delta[W + 1 + t]), at fixed kernel-argument slots so the
+  // kernels read them with constant offsets (batched scalar loads, no waits inside tap loops).
+  int sdelta[kMaxSparse];
 };
 
 struct FwdParams {

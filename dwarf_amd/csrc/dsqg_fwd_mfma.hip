@@ -77,6 +77,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   const int n0w = n0 + 16 * w;
   const int n = n0w + i;  // query row of this lane's MFMA column
   const bool row_ok = n < N;
+  int dl_s[NSM];
+  load_sparse_deltas(p.taps, dl_s);
 
   // ---- Global loads (all zero-filled outside [0, N) by the buffer range check). ----
   // Offsets are (uniform row) * stride + (per-lane part), so the row products stay scalar.
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
   for (int t = 0; t < NH; ++t) {
     if (NSC > 0 || t < NS) {
-      const int m0 = n0w - p.taps.delta[W + 1 + t];
+      const int m0 = n0w - dl_s[t];
 #pragma unroll
       for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
     }
@@ -171,7 +173,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
   for (int t = NH; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
-      const int m0 = n0w - p.taps.delta[W + 1 + t];
+      const int m0 = n0w - dl_s[t];
 #pragma unroll
       for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
     }
@@ -183,7 +185,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
     if (t < NS) {
-      const int r0 = n0w - p.taps.delta[W + 1 + t];
+      const int r0 = n0w - dl_s[t];
 #pragma unroll
       for (int u = 0; u < CHW; ++u) vS[t][u] = bload16(rV, r0 * vsn + vlane[u]);
     }
@@ -240,7 +242,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
       const float v = sRw[i * 16 + t] + sBias2[j];
-      ss[t] = (diag && row_ok && n >= p.taps.delta[j]) ? v : -INFINITY;
+      ss[t] = (diag && row_ok && n >= dl_s[t]) ? v : -INFINITY;
     }
   }
 
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
         }
       }
       if (t + PF < NS) {
-        const int r0 = n0w - p.taps.delta[W + 1 + t + PF];
+        const int r0 = n0w - dl_s[t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) vS[t % PF][u] = bload16(rV, r0 * vsn + vlane[u]);
       }

@@ -91,6 +91,20 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
+// The long-range tap offsets as uniform values, loaded once at kernel start.  The empty asm
+// fixes each value in a scalar register there; left alone, the compiler issues each kernel
+// argument load at its first use inside a tap loop and waits on it (lgkmcnt(0) also waits for
+// every LDS access in flight).
+template <int NSM>
+__device__ __forceinline__ void load_sparse_deltas(const TapTable& taps, int (&sd)[NSM]) {
+#pragma unroll
+  for (int t = 0; t < NSM; ++t) {
+    int v = taps.sdelta[t];
+    asm volatile("" : "+s"(v));
+    sd[t] = v;
+  }
+}
+
 // bf16 operand that holds x in element e (0..3) and zeros elsewhere.
 __device__ __forceinline__ s16x4_t onehot_bf16x4(float x, int e) {
   const __bf16 hb = (__bf16)x;
