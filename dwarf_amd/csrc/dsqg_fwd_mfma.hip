@@ -279,12 +279,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   }
 
   // ---- Long-range P V on the VALU, whole-row layout: o_L[row] += p_t[row] * v_t[row]. ----
-  // The diagonal lanes publish the normalised long-range weights in the wave's table; every
-  // lane then adds p * v for the 16-byte chunk of its rows, with no per-tap LDS round trip.
+  // The diagonal lanes publish the normalised long-range weights in the wave's table (as bf16
+  // in the low half of each word); every lane then adds p * v for the 16-byte chunk of its rows,
+  // with no per-tap LDS round trip.
+  unsigned* sRwU = reinterpret_cast<unsigned*>(sRw);
   if (diag) {
 #pragma unroll
     for (int t = 0; t < NSM; ++t)
-      if (NSC > 0 || t < NS) sRw[i * 16 + t] = ss[t] * inv;
+      if (NSC > 0 || t < NS) sRwU[i * 16 + t] = bf16_bits(ss[t] * inv);
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the weights are in the table
   __builtin_amdgcn_wave_barrier();
@@ -298,13 +300,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     if (NSC > 0 || t < NS) {
 #pragma unroll
       for (int u = 0; u < CHW; ++u) {
-        const float pw = sRw[rc_row<D>(l, u) * 16 + t];
+        // The weight as the bf16 pairs (p, 0) and (0, p): one v_dot2 per element multiplies
+        // and accumulates without unpacking the bf16 V pair (p rounded to bf16, as the MFMA
+        // P V of the dense taps rounds it).
+        const unsigned plo = sRwU[rc_row<D>(l, u) * 16 + t];
+        const unsigned phi = plo << 16;
         const uint4 x = vS[t % PF][u];
         const unsigned wd[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          oL[u][2 * e] = fmaf(pw, __uint_as_float(wd[e] << 16), oL[u][2 * e]);
-          oL[u][2 * e + 1] = fmaf(pw, __uint_as_float(wd[e] & 0xffff0000u), oL[u][2 * e + 1]);
+          oL[u][2 * e] = dot2_bf16(plo, wd[e], oL[u][2 * e]);
+          oL[u][2 * e + 1] = dot2_bf16(phi, wd[e], oL[u][2 * e + 1]);
         }
       }
       if (t + PF < NS) {
