@@ -18,7 +18,7 @@ MAX_OFFSETS = 64
 ABI_VERSION = 1
 
 DSQG_OK, DSQG_EINVAL, DSQG_EUNSUPPORTED, DSQG_EHIP, DSQG_EWORKSPACE = 0, 1, 2, 3, 4
-DSQG_F32, DSQG_BF16 = 0, 1
+DSQG_F32, DSQG_BF16, DSQG_F16 = 0, 1, 2
 
 _i64x4 = ctypes.c_int64 * 4
 _vp = ctypes.c_void_p
@@ -64,6 +64,31 @@ class DecodeArgs(ctypes.Structure):
                 ("out", _vp)]
 
 
+_i64x2 = ctypes.c_int64 * 2
+
+
+class PoolFwdArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("N", ctypes.c_int32), ("C", ctypes.c_int32),
+                ("x_dtype", ctypes.c_int32), ("gate_dtype", ctypes.c_int32),
+                ("out_dtype", ctypes.c_int32),
+                ("x", _vp), ("x_stride", _i64x2),
+                ("gate_pre", _vp), ("gate_stride", _i64x2),
+                ("out", _vp), ("out_stride", _i64x2),
+                ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t)]
+
+
+class PoolBwdArgs(ctypes.Structure):
+    _fields_ = [("B", ctypes.c_int32), ("N", ctypes.c_int32), ("C", ctypes.c_int32),
+                ("x_dtype", ctypes.c_int32), ("gate_dtype", ctypes.c_int32),
+                ("dout_dtype", ctypes.c_int32),
+                ("x", _vp), ("x_stride", _i64x2),
+                ("gate_pre", _vp), ("gate_stride", _i64x2),
+                ("dout", _vp), ("dout_stride", _i64x2),
+                ("dx", _vp), ("dx_stride", _i64x2),
+                ("dgate_pre", _vp), ("dgate_stride", _i64x2),
+                ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t)]
+
+
 # Every symbol include/dsqg.h declares, with its ctypes signature.
 SIGNATURES = {
     "dsqg_abi_version": (ctypes.c_int, []),
@@ -77,6 +102,11 @@ SIGNATURES = {
     "dsqg_bwd_dkdv": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
     "dsqg_bwd_params": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
     "dsqg_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
+    "dsqg_pool_gate_workspace_size": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32,
+                                                     ctypes.c_int32, ctypes.c_int,
+                                                     ctypes.POINTER(ctypes.c_size_t)]),
+    "dsqg_pool_gate_fwd": (ctypes.c_int, [ctypes.POINTER(PoolFwdArgs), _vp]),
+    "dsqg_pool_gate_bwd": (ctypes.c_int, [ctypes.POINTER(PoolBwdArgs), _vp]),
 }
 
 _LIB = None

@@ -11,6 +11,8 @@
 * ``dsqg_attention_qkv(qkv, num_heads, ...)`` -- the same on the projection output
   qkv [B,N,3*H*HD] of train/train_2048_condU.py:169-175: the heads are read in place and the
   gradient comes back as one [B,N,3*H*HD] tensor.
+* ``causal_mean_pool_gate(x, gate_pre)`` -- the interference pool of a DWARF block,
+  train/train_2048_condU.py:289-292: ``sigmoid(gate_pre) * x.cumsum(1) / counts``.
 
 The output [B,H,N,HD] is stored token-major ([B,N,H,HD] memory), so the callers'
 ``out.permute(0, 2, 1, 3).reshape(B, N, H * HD)`` (train/train_2048_condU.py:186) is a view.
@@ -144,6 +146,23 @@ def dsqg_decode_step(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_
     return ops.dsqg_decode(q.contiguous(), k_new.contiguous(), v_new.contiguous(), k_ring,
                            v_ring, pos.to(torch.int64).contiguous(), f32(pos_bias),
                            f32(scale_embed), f32(score_gain), f32(if_gain), list(offs))
+
+
+def causal_mean_pool_gate(x: Tensor, gate_pre: Tensor) -> Tensor:
+    """``sigmoid(gate_pre) * x.cumsum(1) / (n + 1)`` over [B,N,C] (C a multiple of 8), forward
+    and backward on the HIP scan kernels: the interference pool of train/train_2048_condU.py:
+    289-292 (``pool = xi.cumsum(dim=1) / counts``; ``inter = sigmoid(inter_gate(xi)) * pool``).
+
+    x and gate_pre may be float32, bfloat16 or float16 and may differ (under autocast the
+    reference has a float32 LayerNorm output and a float16 gate); the result has their promoted
+    dtype, as the reference's product does, and the sigmoid is rounded to gate_pre's dtype first,
+    as torch's sigmoid of that tensor is.  Sums are fp32 and deterministic.
+    """
+    assert x.dim() == 3, f"x must be [B,N,C], got {tuple(x.shape)}"
+    assert gate_pre.shape == x.shape, (f"gate_pre must match x {tuple(x.shape)}, "
+                                       f"got {tuple(gate_pre.shape)}")
+    assert x.shape[2] % 8 == 0, f"channel count {x.shape[2]} must be a multiple of 8"
+    return ops.pool_gate_fwd(x, gate_pre)
 
 
 class DSQGRingCache:

@@ -7,6 +7,9 @@ State dicts saved from the reference modules load unchanged (``load_state_dict(s
 * ``DSQGAttentionQW``      -- train/train_2048_condU.py:116-205 (adds if_gain) and, with the
   47-offset table, train/train_4096_13m_condU.py:110-175
 * ``DSQGAttentionN_Fused`` -- kernels/dsqg_attention_v2.py:434-471 (pos_bias only, gate bias 2)
+* ``DSQGBlock`` / ``FFN``  -- train/train_2048_condU.py:243-297 (pre-norm block around
+  DSQGAttentionQW; with ``interference=True`` the causal-mean pool feeds the K/V injection,
+  the pool and its gate on the HIP scan kernels)
 
 Forward semantics follow the reference modules: qkv projection, optional Huygens K/V injection
 (``kv_inject=(k_delta, v_delta)`` added to K and V only), DSQG attention, per-head IF gain
@@ -32,10 +35,11 @@ import math
 from typing import Optional, Sequence, Tuple
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import ops
-from .api import DSQGRingCache, dsqg_attention, dsqg_attention_qkv
+from .api import DSQGRingCache, causal_mean_pool_gate, dsqg_attention, dsqg_attention_qkv
 from .offsets import OFFSETS_V3, validate
 
 
@@ -204,3 +208,101 @@ class DSQGAttentionN_Fused(_DSQGBase):
 
     def attn_summary(self) -> dict:
         return self._summary()
+
+
+class FFN(nn.Module):
+    """train/train_2048_condU.py:243-251: fc2(dropout(gelu(fc1(x))))."""
+
+    def __init__(self, embedding_dim: int, ffn_dim: int, dropout: float = 0.1):
+        super().__init__()
+        self.fc1 = nn.Linear(embedding_dim, ffn_dim)
+        self.fc2 = nn.Linear(ffn_dim, embedding_dim)
+        self.drop = nn.Dropout(dropout)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.fc2(self.drop(F.gelu(self.fc1(x))))
+
+
+class DSQGBlockCache:
+    """Decode state of one DSQGBlock: the attention's K/V ring and, with interference, the
+    running fp32 sum of the interference-normed inputs (the causal-mean pool's numerator)."""
+
+    def __init__(self, ring: DSQGRingCache, pool_sum: Optional[Tensor]):
+        self.ring = ring
+        self.pool_sum = pool_sum
+
+
+class DSQGBlock(nn.Module):
+    """train/train_2048_condU.py:260-297: ``x + attn(norm1(x), kv_inject)`` then
+    ``x + ffn(norm2(x))``.  With ``interference=True`` the K/V injection is
+    ``inter_k_proj(inter)`` / ``inter_v_proj(inter)`` of
+    ``inter = sigmoid(inter_gate(xi)) * cumsum(xi) / counts``, ``xi = inter_norm(x)``, the pool
+    and gate fused in one HIP scan (``causal_mean_pool_gate``).  Parameter names and shapes are
+    the reference's, so its state dicts load with ``strict=True``; ``offsets`` selects the
+    attention's table (44 by default).  ``use_checkpoint`` is accepted and, as in the
+    reference's condU block, unused."""
+
+    def __init__(self, embedding_dim: int, num_heads: int, ffn_dim: int, seq_len: int = 2048,
+                 dropout: float = 0.1, use_checkpoint: bool = False, interference: bool = False,
+                 offsets: Optional[Sequence[int]] = None):
+        super().__init__()
+        self.interference = interference
+        self.num_heads = num_heads
+        self.head_dim = embedding_dim // num_heads
+        self.norm1 = nn.LayerNorm(embedding_dim)
+        self.norm2 = nn.LayerNorm(embedding_dim)
+        self.attn = DSQGAttentionQW(embedding_dim, num_heads, seq_len=seq_len, dropout=dropout,
+                                    offsets=offsets)
+        self.ffn = FFN(embedding_dim, ffn_dim, dropout)
+        if interference:
+            self.inter_norm = nn.LayerNorm(embedding_dim)
+            self.inter_gate = nn.Linear(embedding_dim, embedding_dim)
+            self.inter_k_proj = nn.Linear(embedding_dim, embedding_dim)
+            self.inter_v_proj = nn.Linear(embedding_dim, embedding_dim)
+
+    def _inject(self, inter: Tensor):
+        """K/V deltas [B,H,N,HD] (views; the kernels take strides) from inter [B,N,E]."""
+        B, N, _ = inter.shape
+        H, HD = self.num_heads, self.head_dim
+        k_delta = self.inter_k_proj(inter).view(B, N, H, HD).permute(0, 2, 1, 3)
+        v_delta = self.inter_v_proj(inter).view(B, N, H, HD).permute(0, 2, 1, 3)
+        return k_delta, v_delta
+
+    def _forward(self, x: Tensor, cache: Optional[DSQGBlockCache]) -> Tensor:
+        kv_inject = None
+        if self.interference:
+            xi = self.inter_norm(x)
+            kv_inject = self._inject(causal_mean_pool_gate(xi, self.inter_gate(xi)))
+            if cache is not None:
+                cache.pool_sum = xi.detach().float().sum(dim=1)
+        a = self.attn.prefill(self.norm1(x), cache.ring, kv_inject) if cache is not None \
+            else self.attn(self.norm1(x), kv_inject=kv_inject)
+        x = x + a
+        return x + self.ffn(self.norm2(x))
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self._forward(x, None)
+
+    def new_cache(self, batch: int, device=None, dtype=None) -> DSQGBlockCache:
+        return DSQGBlockCache(self.attn.new_cache(batch, device, dtype), None)
+
+    def prefill(self, x: Tensor, cache: DSQGBlockCache) -> Tensor:
+        """forward(x) on a prompt [B,N,E]; loads the K/V ring and the pool's running sum."""
+        return self._forward(x, cache)
+
+    @torch.no_grad()
+    def step(self, x_t: Tensor, cache: DSQGBlockCache) -> Tensor:
+        """Output [B,E] for one new token x_t [B,E] at the cache's position (advances it)."""
+        kv_inject = None
+        if self.interference:
+            B, E = x_t.shape
+            xi = self.inter_norm(x_t)
+            if cache.pool_sum is None:
+                cache.pool_sum = torch.zeros((B, E), dtype=torch.float32, device=x_t.device)
+            cache.pool_sum += xi.float()
+            count = (cache.ring.pos + 1).to(torch.float32).unsqueeze(1)
+            inter = torch.sigmoid(self.inter_gate(xi)) * (cache.pool_sum / count)
+            k_delta, v_delta = self._inject(inter.to(xi.dtype).unsqueeze(1))
+            kv_inject = (k_delta[:, :, 0], v_delta[:, :, 0])
+        x_t = x_t + self.attn.step(self.norm1(x_t), cache.ring, kv_inject)
+        return x_t + self.ffn(self.norm2(x_t))

@@ -1,5 +1,5 @@
 """torch custom ops over the C ABI: ``dwarf::dsqg_fwd``, ``dwarf::dsqg_fwd_qkv``, ``dwarf::dsqg_bwd``,
-``dwarf::dsqg_decode``.
+``dwarf::dsqg_decode``, and the interference pool ``dwarf::pool_gate_fwd`` / ``_bwd``.
 
 The ops take device tensors, pass raw pointers, element strides and the current HIP stream
 to libdsqg_hip.so through ctypes, and allocate their outputs (and the backward workspace) with
@@ -381,3 +381,109 @@ def decode_step_into(q, k_new, v_new, k_ring, v_ring, pos, pos_bias, scale_embed
     a.pos_bias, a.scale_embed, a.score_gain, a.if_gain = (_ptr(t) for t in params)
     a.out = _ptr(out)
     _lib.check(lib.dsqg_decode_step(ctypes.byref(a), _stream(dev)), "dsqg_decode_step")
+
+
+# ------------------------------------------------------------------------------------------
+# Causal-mean pool with a sigmoid gate
+# ------------------------------------------------------------------------------------------
+
+_POOL_CODE = {torch.float32: _lib.DSQG_F32, torch.bfloat16: _lib.DSQG_BF16,
+              torch.float16: _lib.DSQG_F16}
+
+
+def _pool_ready(t: Tensor, B: int, N: int, C: int, name: str) -> Tensor:
+    if tuple(t.shape) != (B, N, C):
+        raise AssertionError(f"{name} must be [{B},{N},{C}], got {tuple(t.shape)}")
+    if t.dtype not in _POOL_CODE:
+        raise AssertionError(f"{name} must be float32, bfloat16 or float16, got {t.dtype}")
+    return _rows_ready(t)
+
+
+def _pool_strides(t: Tensor):
+    return (ctypes.c_int64 * 2)(t.stride(0), t.stride(1))
+
+
+def _pool_workspace(lib, B, N, C, backward: bool, dev) -> Tensor:
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.dsqg_pool_gate_workspace_size(B, N, C, int(backward), ctypes.byref(n)),
+               "dsqg_pool_gate_workspace_size")
+    return torch.empty((max(int(n.value), 1),), dtype=torch.uint8, device=dev)
+
+
+@torch.library.custom_op("dwarf::pool_gate_fwd", mutates_args=())
+def pool_gate_fwd(x: Tensor, gate_pre: Tensor) -> Tensor:
+    """sigmoid(gate_pre) * cumsum(x, 1) / (n + 1) over [B,N,C]; the result has the promoted
+    dtype of x and gate_pre, as the reference's ``sigmoid(inter_gate(xi)) * pool`` does."""
+    dev = _require_gpu(x, gate_pre)
+    lib = _lib.load()
+    B, N, C = x.shape
+    x = _pool_ready(x, B, N, C, "x")
+    g = _pool_ready(gate_pre, B, N, C, "gate_pre")
+    out = torch.empty((B, N, C), dtype=torch.promote_types(x.dtype, g.dtype), device=dev)
+    ws = _pool_workspace(lib, B, N, C, False, dev)
+    a = _lib.PoolFwdArgs()
+    a.B, a.N, a.C = B, N, C
+    a.x_dtype, a.gate_dtype, a.out_dtype = _POOL_CODE[x.dtype], _POOL_CODE[g.dtype], _POOL_CODE[out.dtype]
+    a.x, a.x_stride = _ptr(x), _pool_strides(x)
+    a.gate_pre, a.gate_stride = _ptr(g), _pool_strides(g)
+    a.out, a.out_stride = _ptr(out), _pool_strides(out)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(lib.dsqg_pool_gate_fwd(ctypes.byref(a), _stream(dev)), "dsqg_pool_gate_fwd")
+    return out
+
+
+@pool_gate_fwd.register_fake
+def _(x, gate_pre):
+    return x.new_empty(x.shape, dtype=torch.promote_types(x.dtype, gate_pre.dtype))
+
+
+@torch.library.custom_op("dwarf::pool_gate_bwd", mutates_args=())
+def pool_gate_bwd(x: Tensor, gate_pre: Tensor, dout: Tensor, need_dx: bool,
+                  need_dgate: bool) -> Tuple[Tensor, Tensor]:
+    """(dx in x's dtype, dgate_pre in gate_pre's dtype); an unrequested one is empty."""
+    dev = _require_gpu(x, gate_pre, dout)
+    lib = _lib.load()
+    B, N, C = x.shape
+    x = _pool_ready(x, B, N, C, "x")
+    g = _pool_ready(gate_pre, B, N, C, "gate_pre")
+    dy = _pool_ready(dout, B, N, C, "dout")
+    dx = torch.empty((B, N, C) if need_dx else (0,), dtype=x.dtype, device=dev)
+    dg = torch.empty((B, N, C) if need_dgate else (0,), dtype=g.dtype, device=dev)
+    ws = _pool_workspace(lib, B, N, C, True, dev)
+    a = _lib.PoolBwdArgs()
+    a.B, a.N, a.C = B, N, C
+    a.x_dtype, a.gate_dtype, a.dout_dtype = _POOL_CODE[x.dtype], _POOL_CODE[g.dtype], _POOL_CODE[dy.dtype]
+    a.x, a.x_stride = _ptr(x), _pool_strides(x)
+    a.gate_pre, a.gate_stride = _ptr(g), _pool_strides(g)
+    a.dout, a.dout_stride = _ptr(dy), _pool_strides(dy)
+    if need_dx:
+        a.dx, a.dx_stride = _ptr(dx), _pool_strides(dx)
+    if need_dgate:
+        a.dgate_pre, a.dgate_stride = _ptr(dg), _pool_strides(dg)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    _lib.check(lib.dsqg_pool_gate_bwd(ctypes.byref(a), _stream(dev)), "dsqg_pool_gate_bwd")
+    return dx, dg
+
+
+@pool_gate_bwd.register_fake
+def _(x, gate_pre, dout, need_dx, need_dgate):
+    return (x.new_empty(x.shape if need_dx else (0,)),
+            gate_pre.new_empty(gate_pre.shape if need_dgate else (0,)))
+
+
+def _pool_setup_context(ctx, inputs, output):
+    x, gate_pre = inputs
+    ctx.save_for_backward(x, gate_pre)
+
+
+def _pool_backward(ctx, dout):
+    x, gate_pre = ctx.saved_tensors
+    need_dx, need_dg = bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1])
+    if not (need_dx or need_dg):
+        return None, None
+    dx, dg = pool_gate_bwd(x, gate_pre, dout, need_dx, need_dg)
+    return (dx if need_dx else None), (dg if need_dg else None)
+
+
+torch.library.register_autograd("dwarf::pool_gate_fwd", _pool_backward,
+                                setup_context=_pool_setup_context)

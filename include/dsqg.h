@@ -32,6 +32,9 @@
  *  - dsqg_decode_step: no counterpart in the reference, which regenerates the whole prefix for
  *                       every token (train/train_2048_condU.py:463-487); it realises the
  *                       circular K/V buffer described in README.md:175-177.
+ *  - dsqg_pool_gate_fwd / _bwd <- the interference pool of DSQGBlock.forward,
+ *                       train/train_2048_condU.py:289-292 (cumsum / counts, sigmoid gate), and
+ *                       its autograd backward.
  */
 #ifndef DWARF_DSQG_H
 #define DWARF_DSQG_H
@@ -57,7 +60,8 @@ typedef enum {
     DSQG_EWORKSPACE = 4     /* workspace pointer NULL or smaller than required */
 } dsqg_status;
 
-typedef enum { DSQG_F32 = 0, DSQG_BF16 = 1 } dsqg_dtype;
+/* DSQG_F16 is accepted by the pool entry points only. */
+typedef enum { DSQG_F32 = 0, DSQG_BF16 = 1, DSQG_F16 = 2 } dsqg_dtype;
 
 /* Shape and offset table shared by all entry points. */
 typedef struct {
@@ -162,6 +166,51 @@ int dsqg_bwd_dkdv(const dsqg_bwd_args* args, dsqg_stream_t stream);
 int dsqg_bwd_params(const dsqg_bwd_args* args, dsqg_stream_t stream);
 
 int dsqg_decode_step(const dsqg_decode_args* args, dsqg_stream_t stream);
+
+/* Causal-mean pool with a sigmoid gate (the interference branch of a DWARF block):
+ *
+ *     pool[b,n,c] = (sum_{m<=n} x[b,m,c]) / (n + 1)
+ *     out[b,n,c]  = s[b,n,c] * pool[b,n,c],         s = sigmoid(gate_pre), rounded to gate_dtype
+ *
+ * x, gate_pre and out are [B,N,C] with element strides {b, n} and unit channel stride; C must
+ * be a multiple of 8, base pointers and rows 16-byte aligned.  Each tensor has its own element
+ * type (F32, BF16 or F16); arithmetic is fp32 and the sums are deterministic.  The workspace
+ * (size from dsqg_pool_gate_workspace_size, 256-byte aligned) holds per-chunk column sums.
+ * Replaces train/train_2048_condU.py:289-292 (pool = xi.cumsum(1) / counts;
+ * inter = sigmoid(inter_gate(xi)) * pool). */
+typedef struct {
+    int32_t B, N, C;
+    int32_t x_dtype, gate_dtype, out_dtype;   /* dsqg_dtype each */
+    const void* x;         int64_t x_stride[2];
+    const void* gate_pre;  int64_t gate_stride[2];
+    void* out;             int64_t out_stride[2];
+    void* workspace;
+    size_t workspace_bytes;
+} dsqg_pool_gate_fwd_args;
+
+/* Backward of dsqg_pool_gate_fwd for dout = d out (element type out_dtype):
+ *
+ *     dgate_pre[b,n,c] = dout * pool * s * (1 - s)                 (gate_dtype)
+ *     dx[b,m,c]        = sum_{n>=m} dout[b,n,c] * s[b,n,c] / (n+1)  (x_dtype)
+ *
+ * Either output may be NULL (not computed).  Layout rules as for the forward.
+ * Replaces torch autograd through train/train_2048_condU.py:289-292. */
+typedef struct {
+    int32_t B, N, C;
+    int32_t x_dtype, gate_dtype, dout_dtype;  /* dsqg_dtype each */
+    const void* x;         int64_t x_stride[2];
+    const void* gate_pre;  int64_t gate_stride[2];
+    const void* dout;      int64_t dout_stride[2];
+    void* dx;              int64_t dx_stride[2];
+    void* dgate_pre;       int64_t dgate_stride[2];
+    void* workspace;
+    size_t workspace_bytes;
+} dsqg_pool_gate_bwd_args;
+
+/* Workspace bytes of dsqg_pool_gate_fwd (backward == 0) or _bwd (backward != 0). */
+int dsqg_pool_gate_workspace_size(int32_t B, int32_t N, int32_t C, int backward, size_t* bytes);
+int dsqg_pool_gate_fwd(const dsqg_pool_gate_fwd_args* args, dsqg_stream_t stream);
+int dsqg_pool_gate_bwd(const dsqg_pool_gate_bwd_args* args, dsqg_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,11 @@ def test_ctypes_layout_matches_c(tmp_path):
         "dsqg_bwd_args": (_lib.BwdArgs, ["dout", "lse", "dq_stride", "dpos_bias", "dif_gain",
                                          "workspace", "workspace_bytes"]),
         "dsqg_decode_args": (_lib.DecodeArgs, ["S", "q", "pos", "pos_next", "if_gain", "out"]),
+        "dsqg_pool_gate_fwd_args": (_lib.PoolFwdArgs, ["out_dtype", "x", "gate_stride", "out",
+                                                       "workspace", "workspace_bytes"]),
+        "dsqg_pool_gate_bwd_args": (_lib.PoolBwdArgs, ["dout_dtype", "x", "dout_stride", "dx",
+                                                       "dgate_pre", "dgate_stride", "workspace",
+                                                       "workspace_bytes"]),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
     for cname, (_, fields) in probes.items():
@@ -189,3 +194,61 @@ def test_product_refuses_cpu_tensors():
         dwarf_amd.dsqg_attention_v3(q, q, q, torch.zeros(44, 2), torch.zeros(44, 64))
     with pytest.raises(AssertionError):
         dwarf_amd.dsqg_attention_v3(q, q, q, torch.zeros(43, 2), torch.zeros(44, 64))
+
+
+def _pool_fwd_args(B=2, N=64, C=32, dt=0):
+    from dwarf_amd import _lib
+    a = _lib.PoolFwdArgs()
+    a.B, a.N, a.C = B, N, C
+    a.x_dtype = a.gate_dtype = a.out_dtype = dt
+    fake = 0x10000  # never dereferenced: each case below fails validation first
+    st = (ctypes.c_int64 * 2)(N * C, C)
+    for name in ("x", "gate_pre", "out"):
+        setattr(a, name, fake)
+    a.x_stride, a.gate_stride, a.out_stride = st, st, st
+    return a
+
+
+def test_pool_gate_rejects_bad_arguments(lib):
+    from dwarf_amd import _lib
+    E, W = _lib.DSQG_EINVAL, _lib.DSQG_EWORKSPACE
+    n = ctypes.c_size_t(0)
+    assert lib.dsqg_pool_gate_workspace_size(2, 64, 32, 0, ctypes.byref(n)) == _lib.DSQG_OK
+    n_fwd = n.value
+    assert lib.dsqg_pool_gate_workspace_size(2, 64, 32, 1, ctypes.byref(n)) == _lib.DSQG_OK
+    assert n.value == 2 * n_fwd > 0 and n_fwd % 256 == 0
+    assert lib.dsqg_pool_gate_workspace_size(2, 64, 30, 0, ctypes.byref(n)) == E   # C % 8
+    assert lib.dsqg_pool_gate_workspace_size(-1, 64, 32, 0, ctypes.byref(n)) == E
+    assert lib.dsqg_pool_gate_workspace_size(2, 64, 32, 0, None) == E
+
+    call = lambda a: lib.dsqg_pool_gate_fwd(ctypes.byref(a), None)
+    assert lib.dsqg_pool_gate_fwd(None, None) == E
+    a = _pool_fwd_args(C=12)
+    assert call(a) == E                                   # C must be a multiple of 8
+    a = _pool_fwd_args(); a.gate_dtype = 5
+    assert call(a) == E                                   # unknown element type
+    a = _pool_fwd_args(); a.x = 0x10004
+    assert call(a) == E                                   # misaligned base
+    a = _pool_fwd_args(dt=1); a.gate_stride[1] = 36
+    assert call(a) == E                                   # rows 16-byte aligned
+    a = _pool_fwd_args(); a.out = None
+    assert call(a) == E
+    a = _pool_fwd_args()                                  # valid, but no workspace
+    assert call(a) == W
+    a = _pool_fwd_args(N=0)                               # empty: nothing to do, no launch
+    assert call(a) == _lib.DSQG_OK
+
+    b = _lib.PoolBwdArgs()
+    b.B, b.N, b.C = 2, 64, 32
+    st = (ctypes.c_int64 * 2)(64 * 32, 32)
+    for name in ("x", "gate_pre", "dout", "dx", "dgate_pre"):
+        setattr(b, name, 0x10000)
+        setattr(b, name + "_stride", st)
+    bcall = lambda a: lib.dsqg_pool_gate_bwd(ctypes.byref(a), None)
+    assert bcall(b) == W                                  # valid, but no workspace
+    b.dout_dtype = 9
+    assert bcall(b) == E
+    b.dout_dtype = 0; b.dx = 0x10002
+    assert bcall(b) == E
+    b.dx = None; b.dgate_pre = None                       # nothing requested: no launch
+    assert bcall(b) == _lib.DSQG_OK
