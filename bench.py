@@ -8,7 +8,8 @@ input sets are rotated so that consecutive steps cannot be served from the 256 M
 Prints one JSON line: tok/s (B*N per step), the roofline of the dominant kernel (algorithmic
 bytes per launch over its median launch time, HIP events on the launch stream), the
 fraction of HBM peak for the whole fwd+bwd step, the ring-buffer decode step (workload 4,
-1000 steps replayed from a HIP graph), the drop-in DSQGAttentionQW layer fwd+bwd, and the CPU
+1000 steps replayed from a HIP graph), the drop-in DSQGAttentionQW layer fwd+bwd, the DWARF
+block's interference pool (causal mean times a sigmoid gate) forward and backward, and the CPU
 oracle timed on a bounded sample.
 """
 
@@ -187,6 +188,52 @@ def bench_module(dev, steps=20, warmup=20):
     return res
 
 
+def bench_pool(dev, steps=200, sets=3):
+    """Interference pool of the DWARF block (dsqg_pool_gate_fwd / _bwd: sigmoid(gate) times
+    the causal mean, train/train_2048_condU.py:289-292) at the headline layer's width:
+    x, gate_pre, dout [8,2048,768] bf16, 3 rotating input sets.  Each direction's `steps`
+    calls are captured in one hipGraph and the replay is timed with HIP events, so the figure
+    is GPU time (two kernel launches per call).  Algorithmic bytes: forward reads x and
+    gate_pre and writes out (3 T C E); backward reads x, gate_pre, dout and writes dx,
+    dgate_pre (5 T C E)."""
+    import torch
+    from dwarf_amd import ops
+    B, N, C = 8, 2048, 768
+    g = torch.Generator().manual_seed(2024)
+    calls = []
+    for _ in range(sets):
+        x, gp, dy = ((torch.randn((B, N, C), generator=g) * sc).to(dev, torch.bfloat16)
+                     for sc in (1.0, 2.0, 1.0))
+        calls.append((ops.PoolLaunch(x, gp), ops.PoolLaunch(x, gp, dy)))
+    elem = B * N * C * 2
+    res = {"workload": f"pool+gate x/gate_pre/dout [{B},{N},{C}] bf16", "steps": steps}
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    for name, idx, nbytes in (("fwd", 0, 3 * elem), ("bwd", 1, 5 * elem)):
+        with torch.cuda.stream(s):
+            for i in range(2 * sets):
+                calls[i % sets][idx].run()
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(steps):
+                calls[i % sets][idx].run()
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        st = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        graph.replay()
+        e1.record(st)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / steps
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 3), "algorithmic_bytes": nbytes, "achieved_GBs": round(gbs, 1),
+                     "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    return res
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "hbm_traffic_config2.md")
 
@@ -253,6 +300,7 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
+    ap.add_argument("--no-pool", action="store_true", help="skip the interference-pool leg")
     ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv"], default=None,
                     help="counter-collection mode: launch only this kernel --profile-reps times, "
                          "plus a plain device copy of --copy-mib MiB (the scale reference for "
@@ -372,6 +420,10 @@ def main(argv=None):
         print(f"[bench] module QW fwd+bwd {result['module']['ms_per_step_strided_views']} ms "
               f"(with permute copies {result['module']['ms_per_step_contiguous_copies']} ms)",
               file=sys.stderr, flush=True)
+    if not args.no_pool:
+        result["pool"] = bench_pool(dev)
+        print(f"[bench] pool fwd {result['pool']['fwd']['us']} us, bwd "
+              f"{result['pool']['bwd']['us']} us", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, sets[0][0])

@@ -15,18 +15,27 @@
 //      dout * s / (n+1)), fp32, into the workspace;
 //   2. scan: each workgroup adds the sums of the chunks before it (after it, for the
 //      backward's suffix sum), scans its own rows and writes the outputs.
-// A workgroup is CGT channel groups (8 channels per lane, 16- or 32-byte loads) times
-// RL = 256 / CGT row lanes; a row lane holds RPL consecutive rows in registers, so a chunk is
-// L = RL * RPL rows.  Sums run in a fixed order: results are deterministic.
+// A workgroup is 16 channel groups (4 channels per lane: one 128-byte bf16 row segment per
+// 16 lanes) times 16 row lanes; a row lane holds RPL consecutive rows in registers, so a chunk
+// is L = 16 * RPL rows.  Across the row lanes of a wave the sums and scans are lane shuffles
+// (strides 16 and 32 lanes), across the four waves one LDS exchange; a lane reads every 16th
+// earlier chunk sum.  Every sum runs in a fixed order: results are deterministic.
 //
 // Element types are per tensor (f32, bf16, f16) and uniform per launch, so the type switch at
 // each load is a scalar branch.  As torch computes sigmoid in the gate's dtype, s is rounded
-// to that dtype before it is used; all arithmetic is fp32.
+// to that dtype before it is used; all arithmetic is fp32, with 1/(n+1) and the sigmoid's
+// reciprocal from v_rcp_f32 (1 ulp).
 #include "../../include/dsqg.h"
 #include "dsqg_common.hpp"
 
 namespace dsqg {
 namespace {
+
+constexpr int kCpl = 4;                     // channels per lane
+constexpr int kPoolCgt = 16;                // channel groups (lanes across channels) per workgroup
+constexpr int kPoolCh = kPoolCgt * kCpl;    // 64 channels per workgroup
+constexpr int kPoolRl = kBlock / kPoolCgt;  // 16 row lanes per workgroup, 4 per wave
+constexpr int kWaveRl = 64 / kPoolCgt;
 
 struct PoolParams {
   const void* x;  long long xs_b, xs_n;
@@ -38,7 +47,6 @@ struct PoolParams {
   float* px;      // [B][nchunks][C] chunk sums of x
   float* pp;      // [B][nchunks][C] chunk sums of dout * s / (n+1) (backward)
   int B, N, C;
-  int cgt_log2;   // channel groups (8 channels each) per workgroup, as a power of two
   int nchunks, ctiles, L;
   int xdt, gdt, ydt, odt;  // element types (DSQG_F32 / DSQG_BF16 / DSQG_F16)
 };
@@ -46,65 +54,35 @@ struct PoolParams {
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)h);
 }
-__device__ __forceinline__ uint32_t f32_to_f16(float f) {
-  return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)f);
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b) {
+  return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)a) |
+         ((uint32_t)__builtin_bit_cast(unsigned short, (_Float16)b) << 16);
 }
-
-// Eight channels starting at element offset `off` of a tensor of element type dt.
-__device__ __forceinline__ void load8(const void* base, int dt, long long off, float (&v)[8]) {
-  if (dt == DSQG_F32) {
-    Vec8<float>::load(static_cast<const float*>(base) + off, v);
-    return;
-  }
-  const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + off);
-  const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-  if (dt == DSQG_BF16) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = f16_to_f32(w[i] & 0xffffu);
-      v[2 * i + 1] = f16_to_f32(w[i] >> 16);
-    }
-  }
-}
-
-__device__ __forceinline__ void store8(void* base, int dt, long long off, const float (&v)[8]) {
-  if (dt == DSQG_F32) {
-    Vec8<float>::store(static_cast<float*>(base) + off, v);
-    return;
-  }
-  uint32_t w[4];
-  if (dt == DSQG_BF16) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = f32_to_bf16(v[2 * i]) | (f32_to_bf16(v[2 * i + 1]) << 16);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w[i] = f32_to_f16(v[2 * i]) | (f32_to_f16(v[2 * i + 1]) << 16);
-  }
-  *reinterpret_cast<uint4*>(static_cast<uint16_t*>(base) + off) = make_uint4(w[0], w[1], w[2], w[3]);
+// Two floats -> packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t r;
+  r[0] = (__bf16)a;
+  r[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, r);
 }
 
 // x rounded to element type dt.
 __device__ __forceinline__ float round_to(int dt, float x) {
-  if (dt == DSQG_BF16) return bf16_to_f32(f32_to_bf16(x));
-  if (dt == DSQG_F16) return f16_to_f32(f32_to_f16(x));
+  if (dt == DSQG_BF16) return (float)(__bf16)x;
+  if (dt == DSQG_F16) return (float)(_Float16)x;
   return x;
 }
 
 __device__ __forceinline__ float sigmoid_as(int dt, float g) {
-  return round_to(dt, 1.0f / (1.0f + __expf(-g)));
+  return round_to(dt, __builtin_amdgcn_rcpf(1.0f + __expf(-g)));
 }
 
-// Lane coordinates of a pool workgroup.
+// Lane coordinates: tid = rl * 16 + cgl, so a wave holds 16 channel groups x 4 row lanes.
 struct PoolLane {
-  int b, chunk, cgl, rl, RL, c;  // c: first channel of this lane; active iff c < C
+  int b, chunk, cgl, rl, c;  // c: first channel of this lane; active iff c < C
   bool active;
-  int row0;                      // first of this lane's RPL rows
+  int row0;                  // first of this lane's RPL rows
 };
 
 template <int RPL>
@@ -116,253 +94,316 @@ __device__ __forceinline__ PoolLane pool_lane(const PoolParams& p) {
   q.chunk = bc % p.nchunks;
   q.b = bc / p.nchunks;
   const int tid = threadIdx.x;
-  q.cgl = tid & ((1 << p.cgt_log2) - 1);
-  q.rl = tid >> p.cgt_log2;
-  q.RL = kBlock >> p.cgt_log2;
-  q.c = ((ct << p.cgt_log2) + q.cgl) * 8;
+  q.cgl = tid & (kPoolCgt - 1);
+  q.rl = tid / kPoolCgt;
+  q.c = (ct * kPoolCgt + q.cgl) * kCpl;
   q.active = q.c < p.C;
   q.row0 = q.chunk * p.L + q.rl * RPL;
   return q;
 }
 
-// In-place tree sum over the RL row lanes of an LDS array laid out [RL][CGT*8]; the total for
-// channel group cgl ends in row 0.  Fixed order, so the result is deterministic.
-__device__ __forceinline__ void tree_sum_rows(float* s, int RL, int width, int tid) {
-  for (int half = RL >> 1; half > 0; half >>= 1) {
-    __syncthreads();
-    for (int k = tid; k < half * width; k += kBlock) s[k] += s[k + half * width];
+// Rows of one [B,N,C] operand for this lane: a buffer resource over the batch's slice (its exact
+// extent, so rows >= N read as zero and stores there are dropped), the byte offset of the lane's
+// first row and channel, and the row stride in bytes (uniform, passed as the scalar offset).
+struct TensorRows {
+  __amdgpu_buffer_rsrc_t r;
+  unsigned lane, rstep;
+  int dt;
+};
+
+template <int RPL>
+__device__ __forceinline__ TensorRows rows_of(const void* base, long long sb, long long sn, int dt,
+                                              const PoolParams& p, const PoolLane& q) {
+  const long long es = dt == DSQG_F32 ? 4 : 2;
+  TensorRows t;
+  const char* slice = static_cast<const char*>(base) + (long long)q.b * sb * es;
+  const int ext = p.N > 0 ? (int)(((long long)(p.N - 1) * sn + p.C) * es) : 0;
+  t.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(slice), (short)0, ext, 0x00020000);
+  t.lane = (unsigned)(((long long)q.row0 * sn + q.c) * es);
+  t.rstep = (unsigned)(sn * es);
+  t.dt = dt;
+  return t;
+}
+
+// Channels c..c+3 of row row0 + r (zero beyond the slice).
+__device__ __forceinline__ void tload(const TensorRows& t, int r, float (&v)[kCpl]) {
+  if (t.dt == DSQG_F32) {
+    const float4 a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(t.r, t.lane, r * t.rstep, 0));
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    return;
+  }
+  const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(t.r, t.lane, r * t.rstep, 0));
+  if (t.dt == DSQG_BF16) {
+    v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
+    v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
+  } else {
+    v[0] = f16_to_f32(w.x & 0xffffu); v[1] = f16_to_f32(w.x >> 16);
+    v[2] = f16_to_f32(w.y & 0xffffu); v[3] = f16_to_f32(w.y >> 16);
+  }
+}
+
+// Store channels c..c+3 of row row0 + r (dropped beyond the slice).  Callers skip inactive
+// lanes, whose channels lie past C (inside another row's stride gap).  Stores are at most 8
+// bytes: after a wider VMEM store the hardware needs one wait state before a VALU instruction
+// overwrites the store's data registers, and the compiler was seen to omit it where the store
+// ends a basic block (the next block's first add rewrote the data, so the stored value already
+// held the following row's term).
+__device__ __forceinline__ void tstore(const TensorRows& t, int r, const float (&v)[kCpl]) {
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  if (t.dt == DSQG_F32) {
+    const u32x2 lo = {__float_as_uint(v[0]), __float_as_uint(v[1])};
+    const u32x2 hi = {__float_as_uint(v[2]), __float_as_uint(v[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(lo, t.r, t.lane, r * t.rstep, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(hi, t.r, t.lane + 8, r * t.rstep, 0);
+    return;
+  }
+  u32x2 w;
+  if (t.dt == DSQG_BF16) {
+    w[0] = pack2_bf16(v[0], v[1]);
+    w[1] = pack2_bf16(v[2], v[3]);
+  } else {
+    w[0] = pack2_f16(v[0], v[1]);
+    w[1] = pack2_f16(v[2], v[3]);
+  }
+  __builtin_amdgcn_raw_buffer_store_b64(w, t.r, t.lane, r * t.rstep, 0);
+}
+
+// Total over the 16 row lanes of each of this lane's channels, returned to every lane:
+// shuffles over the wave's 4 row lanes (lane strides 16, 32), then the four wave totals
+// through sW (4 x 64 floats).  Starts with a barrier, so sW may be reused back to back.
+__device__ __forceinline__ void rl_total(float (&v)[kCpl], float* sW) {
+  const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, cgl = tid & (kPoolCgt - 1);
+#pragma unroll
+  for (int off = kPoolCgt; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) v[e] += __shfl_xor(v[e], off, 64);
+  __syncthreads();
+  if (l < kPoolCgt) {
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) sW[w * kPoolCh + cgl * kCpl + e] = v[e];
   }
   __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kCpl; ++e)
+    v[e] = (sW[cgl * kCpl + e] + sW[kPoolCh + cgl * kCpl + e]) +
+           (sW[2 * kPoolCh + cgl * kCpl + e] + sW[3 * kPoolCh + cgl * kCpl + e]);
+}
+
+// Exclusive scan over the 16 row lanes of each channel: the sum of v over the row lanes before
+// this one (SUFFIX: after it).  Shuffle scan within the wave, wave totals through sW.
+template <bool SUFFIX>
+__device__ __forceinline__ void rl_exclusive_scan(float (&v)[kCpl], float* sW) {
+  const int tid = threadIdx.x, l = tid & 63, w = tid >> 6, cgl = tid & (kPoolCgt - 1);
+  const int lr = l / kPoolCgt;  // row lane within the wave
+  float inc[kCpl];
+#pragma unroll
+  for (int e = 0; e < kCpl; ++e) inc[e] = v[e];
+#pragma unroll
+  for (int off = kPoolCgt; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) {
+      const float t = SUFFIX ? __shfl_down(inc[e], off, 64) : __shfl_up(inc[e], off, 64);
+      if (SUFFIX ? (l + off < 64) : (l >= off)) inc[e] += t;
+    }
+  }
+  __syncthreads();
+  if (lr == (SUFFIX ? 0 : kWaveRl - 1)) {
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) sW[w * kPoolCh + cgl * kCpl + e] = inc[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < kCpl; ++e) {
+    float base = 0.f;
+    for (int k = 0; k < 4; ++k)
+      if (SUFFIX ? (k > w) : (k < w)) base += sW[k * kPoolCh + cgl * kCpl + e];
+    v[e] = base + (inc[e] - v[e]);
+  }
+}
+
+// Sum over chunks k = first, first + 16, ... < end of a [B][nchunks][C] partial array.
+__device__ __forceinline__ void strided_chunk_sum(const float* part, const PoolParams& p,
+                                                  const PoolLane& q, int first, int end,
+                                                  float (&acc)[kCpl]) {
+#pragma unroll
+  for (int e = 0; e < kCpl; ++e) acc[e] = 0.f;
+  if (!q.active) return;
+#pragma unroll 4
+  for (int k = first; k < end; k += kPoolRl) {
+    float v[kCpl];
+    const float4 a = *reinterpret_cast<const float4*>(part + ((long long)q.b * p.nchunks + k) * p.C + q.c);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) acc[e] += v[e];
+  }
 }
 
 // ---- Pass 1: chunk sums of x (and, backward, of dout * s / (n+1)). -----------------------
 template <int RPL, bool BWD>
 __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
-  __shared__ float sX[kBlock * 8];
-  __shared__ float sP[BWD ? kBlock * 8 : 1];
+  __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const int width = 8 << p.cgt_log2;
-  float ax[8], ap[8];
+  const TensorRows tx = rows_of<RPL>(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  float ax[kCpl], ap[kCpl];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ax[e] = ap[e] = 0.f;
+  for (int e = 0; e < kCpl; ++e) ax[e] = ap[e] = 0.f;
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
-    const int n = q.row0 + r;
-    if (q.active && n < p.N) {
-      float v[8];
-      load8(p.x, p.xdt, q.b * p.xs_b + n * p.xs_n + q.c, v);
+    float v[kCpl];
+    tload(tx, r, v);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ax[e] += v[e];
-      if constexpr (BWD) {
-        float gv[8], yv[8];
-        load8(p.g, p.gdt, q.b * p.gs_b + n * p.gs_n + q.c, gv);
-        load8(p.dy, p.ydt, q.b * p.ys_b + n * p.ys_n + q.c, yv);
-        const float cnt = (float)(n + 1);
+    for (int e = 0; e < kCpl; ++e) ax[e] += v[e];
+  }
+  if constexpr (BWD) {
+    const TensorRows tg = rows_of<RPL>(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+    const TensorRows ty = rows_of<RPL>(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ap[e] += yv[e] * sigmoid_as(p.gdt, gv[e]) / cnt;
-      }
+    for (int r = 0; r < RPL; ++r) {
+      float gv[kCpl], yv[kCpl];
+      tload(tg, r, gv);
+      tload(ty, r, yv);   // zero beyond N, so those rows add nothing
+      const float inv = __builtin_amdgcn_rcpf((float)(q.row0 + r + 1));
+#pragma unroll
+      for (int e = 0; e < kCpl; ++e) ap[e] += yv[e] * sigmoid_as(p.gdt, gv[e]) * inv;
     }
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    sX[q.rl * width + q.cgl * 8 + e] = ax[e];
-    if constexpr (BWD) sP[q.rl * width + q.cgl * 8 + e] = ap[e];
-  }
-  tree_sum_rows(sX, q.RL, width, threadIdx.x);
-  if constexpr (BWD) tree_sum_rows(sP, q.RL, width, threadIdx.x);
+  rl_total(ax, sW);
+  if constexpr (BWD) rl_total(ap, sW);
   if (q.rl == 0 && q.active) {
     const long long o = ((long long)q.b * p.nchunks + q.chunk) * p.C + q.c;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p.px[o + e] = sX[q.cgl * 8 + e];
-      if constexpr (BWD) p.pp[o + e] = sP[q.cgl * 8 + e];
-    }
-  }
-}
-
-// Sum over chunks k = first, first + RL, ... < end of a [B][nchunks][C] partial array.
-__device__ __forceinline__ void strided_chunk_sum(const float* part, const PoolParams& p,
-                                                  const PoolLane& q, int first, int end,
-                                                  float (&acc)[8]) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  if (!q.active) return;
-  for (int k = first; k < end; k += q.RL) {
-    float v[8];
-    Vec8<float>::load(part + ((long long)q.b * p.nchunks + k) * p.C + q.c, v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += v[e];
+    *reinterpret_cast<float4*>(p.px + o) = make_float4(ax[0], ax[1], ax[2], ax[3]);
+    if constexpr (BWD) *reinterpret_cast<float4*>(p.pp + o) = make_float4(ap[0], ap[1], ap[2], ap[3]);
   }
 }
 
 // ---- Pass 2, forward: out = s * (carry + running sum) / (n+1). ----------------------------
 template <int RPL>
 __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
-  __shared__ float sCarry[kBlock * 8];  // [RL][width] strided sums of earlier chunks
-  __shared__ float sLane[kBlock * 8];   // [RL][width] this chunk's row-lane sums
+  __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const int width = 8 << p.cgt_log2;
-  float x[RPL][8], s[RPL][8];
-  float ls[8];
+  const TensorRows tx = rows_of<RPL>(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  const TensorRows tg = rows_of<RPL>(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+  float x[RPL][kCpl], s[RPL][kCpl];
+  float run[kCpl];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) ls[e] = 0.f;
-#pragma unroll
-  for (int r = 0; r < RPL; ++r) {
-    const int n = q.row0 + r;
-    if (q.active && n < p.N) {
-      float gv[8];
-      load8(p.x, p.xdt, q.b * p.xs_b + n * p.xs_n + q.c, x[r]);
-      load8(p.g, p.gdt, q.b * p.gs_b + n * p.gs_n + q.c, gv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[r][e] = sigmoid_as(p.gdt, gv[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[r][e] = s[r][e] = 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ls[e] += x[r][e];
-  }
-  float cp[8];
-  strided_chunk_sum(p.px, p, q, q.rl, q.chunk, cp);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    sCarry[q.rl * width + q.cgl * 8 + e] = cp[e];
-    sLane[q.rl * width + q.cgl * 8 + e] = ls[e];
-  }
-  __syncthreads();
-  float run[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) run[e] = 0.f;
-  for (int k = 0; k < q.RL; ++k) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) run[e] += sCarry[k * width + q.cgl * 8 + e];
-  }
-  for (int k = 0; k < q.rl; ++k) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) run[e] += sLane[k * width + q.cgl * 8 + e];
-  }
+  for (int e = 0; e < kCpl; ++e) run[e] = 0.f;
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
-    const int n = q.row0 + r;
-    float o[8];
-    const float cnt = (float)(n + 1);
+    float gv[kCpl];
+    tload(tx, r, x[r]);
+    tload(tg, r, gv);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < kCpl; ++e) {
+      s[r][e] = sigmoid_as(p.gdt, gv[e]);
       run[e] += x[r][e];
-      o[e] = s[r][e] * (run[e] / cnt);
     }
-    if (q.active && n < p.N) store8(p.out, p.odt, q.b * p.os_b + n * p.os_n + q.c, o);
+  }
+  float carry[kCpl];
+  strided_chunk_sum(p.px, p, q, q.rl, q.chunk, carry);
+  rl_total(carry, sW);
+  rl_exclusive_scan<false>(run, sW);
+#pragma unroll
+  for (int e = 0; e < kCpl; ++e) run[e] += carry[e];
+  const TensorRows to = rows_of<RPL>(p.out, p.os_b, p.os_n, p.odt, p, q);
+#pragma unroll
+  for (int r = 0; r < RPL; ++r) {
+    const int n = q.row0 + r;
+    const float inv = __builtin_amdgcn_rcpf((float)(n + 1));
+    float o[kCpl];
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) {
+      run[e] += x[r][e];
+      o[e] = s[r][e] * (run[e] * inv);
+    }
+    if (q.active) tstore(to, r, o);
   }
 }
 
 // ---- Pass 2, backward. ----------------------------------------------------------------------
 template <int RPL>
 __global__ __launch_bounds__(kBlock) void pool_bwd_scan_kernel(PoolParams p) {
-  __shared__ float sCx[kBlock * 8];  // strided sums of x over earlier chunks
-  __shared__ float sLx[kBlock * 8];  // row-lane sums of x
-  __shared__ float sCp[kBlock * 8];  // strided sums of dP over later chunks
-  __shared__ float sLp[kBlock * 8];  // row-lane sums of dP
+  __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const int width = 8 << p.cgt_log2;
-  float x[RPL][8], s[RPL][8], y[RPL][8];
-  float lx[8], lp[8];
+  const TensorRows tx = rows_of<RPL>(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  const TensorRows tg = rows_of<RPL>(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+  const TensorRows ty = rows_of<RPL>(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
+  float x[RPL][kCpl], s[RPL][kCpl], y[RPL][kCpl];
+  float runx[kCpl], runp[kCpl];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) lx[e] = lp[e] = 0.f;
+  for (int e = 0; e < kCpl; ++e) runx[e] = runp[e] = 0.f;
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     const int n = q.row0 + r;
-    if (q.active && n < p.N) {
-      float gv[8];
-      load8(p.x, p.xdt, q.b * p.xs_b + n * p.xs_n + q.c, x[r]);
-      load8(p.g, p.gdt, q.b * p.gs_b + n * p.gs_n + q.c, gv);
-      load8(p.dy, p.ydt, q.b * p.ys_b + n * p.ys_n + q.c, y[r]);
+    float gv[kCpl];
+    tload(tx, r, x[r]);
+    tload(tg, r, gv);
+    tload(ty, r, y[r]);   // zero beyond N: those rows add nothing below
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s[r][e] = sigmoid_as(p.gdt, gv[e]);
-    } else {
+    for (int e = 0; e < kCpl; ++e) s[r][e] = sigmoid_as(p.gdt, gv[e]);
+    const float inv = __builtin_amdgcn_rcpf((float)(n + 1));
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[r][e] = s[r][e] = y[r][e] = 0.f;
-    }
-    const float cnt = (float)(n + 1);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      lx[e] += x[r][e];
-      lp[e] += y[r][e] * s[r][e] / cnt;
+    for (int e = 0; e < kCpl; ++e) {
+      runx[e] += x[r][e];
+      runp[e] += y[r][e] * s[r][e] * inv;   // dout * s / (n+1), recomputed the same way below
     }
   }
-  float cx[8], cp[8];
+  float cx[kCpl], cp[kCpl];
   strided_chunk_sum(p.px, p, q, q.rl, q.chunk, cx);
   strided_chunk_sum(p.pp, p, q, q.chunk + 1 + q.rl, p.nchunks, cp);
+  rl_total(cx, sW);
+  rl_total(cp, sW);
+  rl_exclusive_scan<false>(runx, sW);
+  rl_exclusive_scan<true>(runp, sW);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int o = q.rl * width + q.cgl * 8 + e;
-    sCx[o] = cx[e]; sLx[o] = lx[e]; sCp[o] = cp[e]; sLp[o] = lp[e];
+  for (int e = 0; e < kCpl; ++e) {
+    runx[e] += cx[e];
+    runp[e] += cp[e];
   }
-  __syncthreads();
-  float runx[8], runp[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) runx[e] = runp[e] = 0.f;
-  for (int k = 0; k < q.RL; ++k) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      runx[e] += sCx[k * width + q.cgl * 8 + e];
-      runp[e] += sCp[k * width + q.cgl * 8 + e];
-    }
-  }
-  for (int k = 0; k < q.rl; ++k) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) runx[e] += sLx[k * width + q.cgl * 8 + e];
-  }
-  for (int k = q.RL - 1; k > q.rl; --k) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) runp[e] += sLp[k * width + q.cgl * 8 + e];
-  }
+  const TensorRows tdg = rows_of<RPL>(p.dg ? p.dg : p.x, p.dgs_b, p.dgs_n, p.gdt, p, q);
+  const TensorRows tdx = rows_of<RPL>(p.dx ? p.dx : p.x, p.dxs_b, p.dxs_n, p.xdt, p, q);
   // dgate_pre on the way down the rows (prefix sums of x) ...
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     const int n = q.row0 + r;
-    const float cnt = (float)(n + 1);
-    float o[8];
+    const float inv = __builtin_amdgcn_rcpf((float)(n + 1));
+    float o[kCpl];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < kCpl; ++e) {
       runx[e] += x[r][e];
-      o[e] = y[r][e] * (runx[e] / cnt) * (s[r][e] * (1.0f - s[r][e]));
+      o[e] = y[r][e] * (runx[e] * inv) * (s[r][e] * (1.0f - s[r][e]));
     }
-    if (p.dg && q.active && n < p.N) store8(p.dg, p.gdt, q.b * p.dgs_b + n * p.dgs_n + q.c, o);
+    if (p.dg && q.active) tstore(tdg, r, o);
   }
   // ... and dx on the way up (suffix sums of dout * s / (n+1)).
 #pragma unroll
   for (int r = RPL - 1; r >= 0; --r) {
     const int n = q.row0 + r;
-    const float cnt = (float)(n + 1);
-    float o[8];
+    const float inv = __builtin_amdgcn_rcpf((float)(n + 1));
+    float o[kCpl];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      runp[e] += y[r][e] * s[r][e] / cnt;
+    for (int e = 0; e < kCpl; ++e) {
+      runp[e] += y[r][e] * s[r][e] * inv;
       o[e] = runp[e];
     }
-    if (p.dx && q.active && n < p.N) store8(p.dx, p.xdt, q.b * p.dxs_b + n * p.dxs_n + q.c, o);
+    if (p.dx && q.active) tstore(tdx, r, o);
   }
 }
 
 // ---- Host side. ------------------------------------------------------------------------------
 
 struct PoolPlan {
-  int cgt_log2, rpl, L, nchunks, ctiles;
+  int rpl, L, nchunks, ctiles;
   long long grid;
 };
 
-// Channel groups per workgroup: the smallest power of two covering C/8, at most 64; rows per
-// lane: the most (4, 2, 1) that still gives at least 1024 workgroups.
-PoolPlan pool_plan(int B, int N, int C) {
+// 64 channels per workgroup; rows per lane: the most (4, 2, 1; the backward at most 2, which
+// keeps it at 100 VGPRs) that still gives at least 1024 workgroups.
+PoolPlan pool_plan(int B, int N, int C, bool bwd) {
   PoolPlan pl;
-  const int cg = C / 8;
-  pl.cgt_log2 = 0;
-  while ((1 << pl.cgt_log2) < cg && pl.cgt_log2 < 6) ++pl.cgt_log2;
-  pl.ctiles = (cg + (1 << pl.cgt_log2) - 1) >> pl.cgt_log2;
-  const int RL = kBlock >> pl.cgt_log2;
-  for (int rpl = 4; rpl >= 1; rpl >>= 1) {
+  pl.ctiles = (C + kPoolCh - 1) / kPoolCh;
+  for (int rpl = bwd ? 2 : 4; rpl >= 1; rpl >>= 1) {
     pl.rpl = rpl;
-    pl.L = RL * rpl;
+    pl.L = kPoolRl * rpl;
     pl.nchunks = (N + pl.L - 1) / pl.L;
     pl.grid = (long long)B * pl.nchunks * pl.ctiles;
     if (pl.grid >= 1024) break;
@@ -374,13 +415,17 @@ bool pool_dtype_ok(int dt) { return dt == DSQG_F32 || dt == DSQG_BF16 || dt == D
 size_t pool_elem(int dt) { return dt == DSQG_F32 ? 4 : 2; }
 size_t align256_p(size_t x) { return (x + 255) & ~size_t(255); }
 
-// A [B,N,C] operand: 16-byte aligned base and rows, non-negative strides.
-bool pool_tensor_ok(const void* ptr, const int64_t st[2], int dt) {
-  if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 15u)) return false;
+// A [B,N,C] operand: 16-byte aligned base and rows, non-negative batch stride, rows that do
+// not overlap (row stride >= C) and a batch slice of less than 2 GiB (the kernels address a
+// slice with 32-bit buffer offsets).
+int pool_tensor_check(const void* ptr, const int64_t st[2], int dt, int N, int C) {
+  if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 15u)) return DSQG_EINVAL;
   const long long es = (long long)pool_elem(dt);
   for (int i = 0; i < 2; ++i)
-    if (st[i] < 0 || (st[i] * es) % 16 != 0) return false;
-  return true;
+    if (st[i] < 0 || (st[i] * es) % 16 != 0) return DSQG_EINVAL;
+  if (st[1] < C) return DSQG_EINVAL;
+  if (((long long)(N - 1) * st[1] + C) * es >= (1ll << 31)) return DSQG_EUNSUPPORTED;
+  return DSQG_OK;
 }
 
 int pool_shape_ok(int B, int N, int C) {
@@ -390,24 +435,25 @@ int pool_shape_ok(int B, int N, int C) {
 }
 
 size_t pool_workspace(int B, int N, int C, bool bwd) {
-  const PoolPlan pl = pool_plan(B, N, C);
+  const PoolPlan pl = pool_plan(B, N, C, bwd);
   const size_t one = align256_p(sizeof(float) * (size_t)B * pl.nchunks * C);
   return bwd ? 2 * one : one;
 }
 
 template <int RPL>
-void launch_pool(const PoolParams& p, bool bwd, unsigned grid, hipStream_t st) {
-  if (bwd) {
-    hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, true>), dim3(grid), dim3(kBlock), 0, st, p);
-    hipLaunchKernelGGL((pool_bwd_scan_kernel<RPL>), dim3(grid), dim3(kBlock), 0, st, p);
-  } else {
-    hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, false>), dim3(grid), dim3(kBlock), 0, st, p);
-    hipLaunchKernelGGL((pool_fwd_scan_kernel<RPL>), dim3(grid), dim3(kBlock), 0, st, p);
-  }
+void launch_pool_fwd(const PoolParams& p, unsigned grid, hipStream_t st) {
+  hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, false>), dim3(grid), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((pool_fwd_scan_kernel<RPL>), dim3(grid), dim3(kBlock), 0, st, p);
+}
+
+template <int RPL>
+void launch_pool_bwd(const PoolParams& p, unsigned grid, hipStream_t st) {
+  hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, true>), dim3(grid), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((pool_bwd_scan_kernel<RPL>), dim3(grid), dim3(kBlock), 0, st, p);
 }
 
 int run_pool(PoolParams& p, bool bwd, void* ws, size_t ws_bytes, hipStream_t st) {
-  const PoolPlan pl = pool_plan(p.B, p.N, p.C);
+  const PoolPlan pl = pool_plan(p.B, p.N, p.C, bwd);
   if (pl.grid == 0) return DSQG_OK;
   if (pl.grid > 0x7fffffffll) return DSQG_EUNSUPPORTED;
   const size_t one = align256_p(sizeof(float) * (size_t)p.B * pl.nchunks * p.C);
@@ -415,14 +461,17 @@ int run_pool(PoolParams& p, bool bwd, void* ws, size_t ws_bytes, hipStream_t st)
     return DSQG_EWORKSPACE;
   p.px = static_cast<float*>(ws);
   p.pp = bwd ? reinterpret_cast<float*>(static_cast<char*>(ws) + one) : nullptr;
-  p.cgt_log2 = pl.cgt_log2;
   p.nchunks = pl.nchunks;
   p.ctiles = pl.ctiles;
   p.L = pl.L;
-  switch (pl.rpl) {
-    case 4: launch_pool<4>(p, bwd, (unsigned)pl.grid, st); break;
-    case 2: launch_pool<2>(p, bwd, (unsigned)pl.grid, st); break;
-    default: launch_pool<1>(p, bwd, (unsigned)pl.grid, st); break;
+  const unsigned grid = (unsigned)pl.grid;
+  if (bwd) {
+    if (pl.rpl == 2) launch_pool_bwd<2>(p, grid, st);
+    else launch_pool_bwd<1>(p, grid, st);
+  } else {
+    if (pl.rpl == 4) launch_pool_fwd<4>(p, grid, st);
+    else if (pl.rpl == 2) launch_pool_fwd<2>(p, grid, st);
+    else launch_pool_fwd<1>(p, grid, st);
   }
   return hipGetLastError() == hipSuccess ? DSQG_OK : DSQG_EHIP;
 }
@@ -448,10 +497,10 @@ extern "C" int dsqg_pool_gate_fwd(const dsqg_pool_gate_fwd_args* a, dsqg_stream_
   if (!pool_dtype_ok(a->x_dtype) || !pool_dtype_ok(a->gate_dtype) || !pool_dtype_ok(a->out_dtype))
     return DSQG_EINVAL;
   if ((long long)a->B * a->N == 0) return DSQG_OK;
-  if (!pool_tensor_ok(a->x, a->x_stride, a->x_dtype) ||
-      !pool_tensor_ok(a->gate_pre, a->gate_stride, a->gate_dtype) ||
-      !pool_tensor_ok(a->out, a->out_stride, a->out_dtype))
-    return DSQG_EINVAL;
+  if ((rc = pool_tensor_check(a->x, a->x_stride, a->x_dtype, a->N, a->C)) != DSQG_OK ||
+      (rc = pool_tensor_check(a->gate_pre, a->gate_stride, a->gate_dtype, a->N, a->C)) != DSQG_OK ||
+      (rc = pool_tensor_check(a->out, a->out_stride, a->out_dtype, a->N, a->C)) != DSQG_OK)
+    return rc;
   PoolParams p = {};
   p.x = a->x; p.xs_b = a->x_stride[0]; p.xs_n = a->x_stride[1];
   p.g = a->gate_pre; p.gs_b = a->gate_stride[0]; p.gs_n = a->gate_stride[1];
@@ -468,18 +517,20 @@ extern "C" int dsqg_pool_gate_bwd(const dsqg_pool_gate_bwd_args* a, dsqg_stream_
   if (!pool_dtype_ok(a->x_dtype) || !pool_dtype_ok(a->gate_dtype) || !pool_dtype_ok(a->dout_dtype))
     return DSQG_EINVAL;
   if ((long long)a->B * a->N == 0 || (!a->dx && !a->dgate_pre)) return DSQG_OK;
-  if (!pool_tensor_ok(a->x, a->x_stride, a->x_dtype) ||
-      !pool_tensor_ok(a->gate_pre, a->gate_stride, a->gate_dtype) ||
-      !pool_tensor_ok(a->dout, a->dout_stride, a->dout_dtype) ||
-      (a->dx && !pool_tensor_ok(a->dx, a->dx_stride, a->x_dtype)) ||
-      (a->dgate_pre && !pool_tensor_ok(a->dgate_pre, a->dgate_stride, a->gate_dtype)))
-    return DSQG_EINVAL;
+  if ((rc = pool_tensor_check(a->x, a->x_stride, a->x_dtype, a->N, a->C)) != DSQG_OK ||
+      (rc = pool_tensor_check(a->gate_pre, a->gate_stride, a->gate_dtype, a->N, a->C)) != DSQG_OK ||
+      (rc = pool_tensor_check(a->dout, a->dout_stride, a->dout_dtype, a->N, a->C)) != DSQG_OK ||
+      (a->dx && (rc = pool_tensor_check(a->dx, a->dx_stride, a->x_dtype, a->N, a->C)) != DSQG_OK) ||
+      (a->dgate_pre &&
+       (rc = pool_tensor_check(a->dgate_pre, a->dgate_stride, a->gate_dtype, a->N, a->C)) != DSQG_OK))
+    return rc;
   PoolParams p = {};
   p.x = a->x; p.xs_b = a->x_stride[0]; p.xs_n = a->x_stride[1];
   p.g = a->gate_pre; p.gs_b = a->gate_stride[0]; p.gs_n = a->gate_stride[1];
   p.dy = a->dout; p.ys_b = a->dout_stride[0]; p.ys_n = a->dout_stride[1];
-  p.dx = a->dx; p.dxs_b = a->dx_stride[0]; p.dxs_n = a->dx_stride[1];
-  p.dg = a->dgate_pre; p.dgs_b = a->dgate_stride[0]; p.dgs_n = a->dgate_stride[1];
+  p.dx = a->dx; p.dxs_b = a->dx ? a->dx_stride[0] : 0; p.dxs_n = a->dx ? a->dx_stride[1] : p.C;
+  p.dg = a->dgate_pre;
+  p.dgs_b = a->dgate_pre ? a->dgate_stride[0] : 0; p.dgs_n = a->dgate_pre ? a->dgate_stride[1] : p.C;
   p.B = a->B; p.N = a->N; p.C = a->C;
   p.xdt = a->x_dtype; p.gdt = a->gate_dtype; p.ydt = a->dout_dtype; p.odt = a->dout_dtype;
   return run_pool(p, true, a->workspace, a->workspace_bytes, reinterpret_cast<hipStream_t>(stream));

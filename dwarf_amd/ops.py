@@ -396,6 +396,8 @@ def _pool_ready(t: Tensor, B: int, N: int, C: int, name: str) -> Tensor:
         raise AssertionError(f"{name} must be [{B},{N},{C}], got {tuple(t.shape)}")
     if t.dtype not in _POOL_CODE:
         raise AssertionError(f"{name} must be float32, bfloat16 or float16, got {t.dtype}")
+    if t.numel() and t.stride(1) < C:  # overlapping rows (e.g. expanded along N): copy
+        t = t.contiguous()
     return _rows_ready(t)
 
 
@@ -410,26 +412,62 @@ def _pool_workspace(lib, B, N, C, backward: bool, dev) -> Tensor:
     return torch.empty((max(int(n.value), 1),), dtype=torch.uint8, device=dev)
 
 
+class PoolLaunch:
+    """Argument block, outputs and workspace of one pool call, reusable: ``run()`` relaunches it.
+
+    Forward when ``dout`` is None (``out``), else backward (``dx`` / ``dgate``, empty when not
+    requested).  Every tensor is [B,N,C]; strided views are read in place when their rows are
+    16-byte aligned.
+    """
+
+    def __init__(self, x: Tensor, gate_pre: Tensor, dout: Optional[Tensor] = None,
+                 need_dx: bool = True, need_dgate: bool = True):
+        dev = _require_gpu(x, gate_pre, dout)
+        self.lib = _lib.load()
+        self.device = dev
+        B, N, C = x.shape
+        x = _pool_ready(x, B, N, C, "x")
+        g = _pool_ready(gate_pre, B, N, C, "gate_pre")
+        self.backward = dout is not None
+        self.ws = _pool_workspace(self.lib, B, N, C, self.backward, dev)
+        if not self.backward:
+            self.out = torch.empty((B, N, C), dtype=torch.promote_types(x.dtype, g.dtype),
+                                   device=dev)
+            a = _lib.PoolFwdArgs()
+            a.out_dtype = _POOL_CODE[self.out.dtype]
+            a.out, a.out_stride = _ptr(self.out), _pool_strides(self.out)
+            self._keep = (x, g)
+        else:
+            dy = _pool_ready(dout, B, N, C, "dout")
+            self.dx = torch.empty((B, N, C) if need_dx else (0,), dtype=x.dtype, device=dev)
+            self.dgate = torch.empty((B, N, C) if need_dgate else (0,), dtype=g.dtype, device=dev)
+            a = _lib.PoolBwdArgs()
+            a.dout_dtype = _POOL_CODE[dy.dtype]
+            a.dout, a.dout_stride = _ptr(dy), _pool_strides(dy)
+            if need_dx:
+                a.dx, a.dx_stride = _ptr(self.dx), _pool_strides(self.dx)
+            if need_dgate:
+                a.dgate_pre, a.dgate_stride = _ptr(self.dgate), _pool_strides(self.dgate)
+            self._keep = (x, g, dy)
+        a.B, a.N, a.C = B, N, C
+        a.x_dtype, a.gate_dtype = _POOL_CODE[x.dtype], _POOL_CODE[g.dtype]
+        a.x, a.x_stride = _ptr(x), _pool_strides(x)
+        a.gate_pre, a.gate_stride = _ptr(g), _pool_strides(g)
+        a.workspace, a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        self.args = a
+
+    def run(self) -> None:
+        name = "dsqg_pool_gate_bwd" if self.backward else "dsqg_pool_gate_fwd"
+        _lib.check(getattr(self.lib, name)(ctypes.byref(self.args), _stream(self.device)), name)
+
+
 @torch.library.custom_op("dwarf::pool_gate_fwd", mutates_args=())
 def pool_gate_fwd(x: Tensor, gate_pre: Tensor) -> Tensor:
     """sigmoid(gate_pre) * cumsum(x, 1) / (n + 1) over [B,N,C]; the result has the promoted
     dtype of x and gate_pre, as the reference's ``sigmoid(inter_gate(xi)) * pool`` does."""
-    dev = _require_gpu(x, gate_pre)
-    lib = _lib.load()
-    B, N, C = x.shape
-    x = _pool_ready(x, B, N, C, "x")
-    g = _pool_ready(gate_pre, B, N, C, "gate_pre")
-    out = torch.empty((B, N, C), dtype=torch.promote_types(x.dtype, g.dtype), device=dev)
-    ws = _pool_workspace(lib, B, N, C, False, dev)
-    a = _lib.PoolFwdArgs()
-    a.B, a.N, a.C = B, N, C
-    a.x_dtype, a.gate_dtype, a.out_dtype = _POOL_CODE[x.dtype], _POOL_CODE[g.dtype], _POOL_CODE[out.dtype]
-    a.x, a.x_stride = _ptr(x), _pool_strides(x)
-    a.gate_pre, a.gate_stride = _ptr(g), _pool_strides(g)
-    a.out, a.out_stride = _ptr(out), _pool_strides(out)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    _lib.check(lib.dsqg_pool_gate_fwd(ctypes.byref(a), _stream(dev)), "dsqg_pool_gate_fwd")
-    return out
+    launch = PoolLaunch(x, gate_pre)
+    launch.run()
+    return launch.out
 
 
 @pool_gate_fwd.register_fake
@@ -441,28 +479,9 @@ def _(x, gate_pre):
 def pool_gate_bwd(x: Tensor, gate_pre: Tensor, dout: Tensor, need_dx: bool,
                   need_dgate: bool) -> Tuple[Tensor, Tensor]:
     """(dx in x's dtype, dgate_pre in gate_pre's dtype); an unrequested one is empty."""
-    dev = _require_gpu(x, gate_pre, dout)
-    lib = _lib.load()
-    B, N, C = x.shape
-    x = _pool_ready(x, B, N, C, "x")
-    g = _pool_ready(gate_pre, B, N, C, "gate_pre")
-    dy = _pool_ready(dout, B, N, C, "dout")
-    dx = torch.empty((B, N, C) if need_dx else (0,), dtype=x.dtype, device=dev)
-    dg = torch.empty((B, N, C) if need_dgate else (0,), dtype=g.dtype, device=dev)
-    ws = _pool_workspace(lib, B, N, C, True, dev)
-    a = _lib.PoolBwdArgs()
-    a.B, a.N, a.C = B, N, C
-    a.x_dtype, a.gate_dtype, a.dout_dtype = _POOL_CODE[x.dtype], _POOL_CODE[g.dtype], _POOL_CODE[dy.dtype]
-    a.x, a.x_stride = _ptr(x), _pool_strides(x)
-    a.gate_pre, a.gate_stride = _ptr(g), _pool_strides(g)
-    a.dout, a.dout_stride = _ptr(dy), _pool_strides(dy)
-    if need_dx:
-        a.dx, a.dx_stride = _ptr(dx), _pool_strides(dx)
-    if need_dgate:
-        a.dgate_pre, a.dgate_stride = _ptr(dg), _pool_strides(dg)
-    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-    _lib.check(lib.dsqg_pool_gate_bwd(ctypes.byref(a), _stream(dev)), "dsqg_pool_gate_bwd")
-    return dx, dg
+    launch = PoolLaunch(x, gate_pre, dout, need_dx, need_dgate)
+    launch.run()
+    return launch.dx, launch.dgate
 
 
 @pool_gate_bwd.register_fake

@@ -173,7 +173,8 @@ int dsqg_decode_step(const dsqg_decode_args* args, dsqg_stream_t stream);
  *     out[b,n,c]  = s[b,n,c] * pool[b,n,c],         s = sigmoid(gate_pre), rounded to gate_dtype
  *
  * x, gate_pre and out are [B,N,C] with element strides {b, n} and unit channel stride; C must
- * be a multiple of 8, base pointers and rows 16-byte aligned.  Each tensor has its own element
+ * be a multiple of 8, base pointers and rows 16-byte aligned, the row stride at least C (rows do
+ * not overlap) and one batch slice under 2 GiB (EUNSUPPORTED otherwise).  Each tensor has its own element
  * type (F32, BF16 or F16); arithmetic is fp32 and the sums are deterministic.  The workspace
  * (size from dsqg_pool_gate_workspace_size, 256-byte aligned) holds per-chunk column sums.
  * Replaces train/train_2048_condU.py:289-292 (pool = xi.cumsum(1) / counts;

@@ -216,7 +216,7 @@ def test_pool_gate_rejects_bad_arguments(lib):
     assert lib.dsqg_pool_gate_workspace_size(2, 64, 32, 0, ctypes.byref(n)) == _lib.DSQG_OK
     n_fwd = n.value
     assert lib.dsqg_pool_gate_workspace_size(2, 64, 32, 1, ctypes.byref(n)) == _lib.DSQG_OK
-    assert n.value == 2 * n_fwd > 0 and n_fwd % 256 == 0
+    assert n.value > 0 and n_fwd > 0 and n_fwd % 256 == 0 and n.value % 256 == 0
     assert lib.dsqg_pool_gate_workspace_size(2, 64, 30, 0, ctypes.byref(n)) == E   # C % 8
     assert lib.dsqg_pool_gate_workspace_size(-1, 64, 32, 0, ctypes.byref(n)) == E
     assert lib.dsqg_pool_gate_workspace_size(2, 64, 32, 0, None) == E
@@ -233,6 +233,8 @@ def test_pool_gate_rejects_bad_arguments(lib):
     assert call(a) == E                                   # rows 16-byte aligned
     a = _pool_fwd_args(); a.out = None
     assert call(a) == E
+    a = _pool_fwd_args(); a.x_stride[1] = 16
+    assert call(a) == E                                   # overlapping rows (stride < C)
     a = _pool_fwd_args()                                  # valid, but no workspace
     assert call(a) == W
     a = _pool_fwd_args(N=0)                               # empty: nothing to do, no launch
@@ -241,9 +243,10 @@ def test_pool_gate_rejects_bad_arguments(lib):
     b = _lib.PoolBwdArgs()
     b.B, b.N, b.C = 2, 64, 32
     st = (ctypes.c_int64 * 2)(64 * 32, 32)
-    for name in ("x", "gate_pre", "dout", "dx", "dgate_pre"):
+    for name, sname in (("x", "x"), ("gate_pre", "gate"), ("dout", "dout"), ("dx", "dx"),
+                        ("dgate_pre", "dgate")):
         setattr(b, name, 0x10000)
-        setattr(b, name + "_stride", st)
+        setattr(b, sname + "_stride", st)
     bcall = lambda a: lib.dsqg_pool_gate_bwd(ctypes.byref(a), None)
     assert bcall(b) == W                                  # valid, but no workspace
     b.dout_dtype = 9

@@ -82,8 +82,8 @@ def test_pool_gate_matches_oracle(gpu_device, shape, xdt, gdt):
 
 
 def test_pool_gate_strided_views(gpu_device):
-    """x a channel slice of a wider tensor, gate_pre a permuted [N,B,C] buffer, dout expanded
-    along B and N (zero strides): all read in place through their strides."""
+    """x a channel slice of a wider tensor and gate_pre a permuted [N,B,C] buffer, read in place
+    through their strides; dout expanded along B and N (zero strides, copied by the op)."""
     B, N, C = 3, 333, 64
     _say("strided views")
     g = torch.Generator().manual_seed(3)
