@@ -9,8 +9,9 @@ Prints one JSON line: tok/s (B*N per step), the roofline of the dominant kernel 
 bytes per launch over its median launch time, HIP events on the launch stream), the
 fraction of HBM peak for the whole fwd+bwd step, the ring-buffer decode step (workload 4,
 1000 steps replayed from a HIP graph), the drop-in DSQGAttentionQW layer fwd+bwd, the DWARF
-block's interference pool (causal mean times a sigmoid gate) forward and backward, and the CPU
-oracle timed on a bounded sample.
+block's interference pool (causal mean times a sigmoid gate) forward and backward, greedy
+generation with the condU 13M model (incremental vs the reference's full recomputation), and
+the CPU oracle timed on a bounded sample.
 """
 
 from __future__ import annotations
@@ -234,6 +235,45 @@ def bench_pool(dev, steps=200, sets=3):
     return res
 
 
+def bench_generation(dev, prompt=1024, new_tokens=64, ref_tokens=16):
+    """Greedy generation with the condU 13M model (train/train_2048_condU.py:55-67: vocab 32000,
+    E 256, 6 layers, 8 heads, FFN 1024, seq_len 2048; random weights, bf16), one sequence:
+    CondMTransformer.generate (prefill once, then one decode step per layer and token) against
+    the reference's loop, which runs the whole model on the sequence for every token
+    (train/train_2048_condU.py:463-487), timed on `ref_tokens` tokens."""
+    import torch
+    from dwarf_amd.generation import CondMTransformer
+    torch.manual_seed(13)
+    m = CondMTransformer(32000, 256, 6, 8, 1024, 2048, dropout=0.0).to(dev, torch.bfloat16).eval()
+    ids = torch.randint(0, 32000, (1, prompt), device=dev)
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = fn()
+        torch.cuda.synchronize()
+        return out, time.perf_counter() - t0
+
+    m.generate(ids[:, :64], 4, temperature=0.0)  # warm-up
+    out, t_inc = timed(lambda: m.generate(ids, new_tokens, temperature=0.0))
+
+    def reference_loop():
+        x = ids
+        with torch.no_grad():
+            for _ in range(ref_tokens):
+                nxt = m(x[:, -m.seq_len:])[:, -1].argmax(-1, keepdim=True)
+                x = torch.cat([x, nxt], dim=1)
+        return x
+
+    reference_loop()  # warm-up
+    ref, t_ref = timed(reference_loop)
+    return {"workload": f"condU 13M (V32000 E256 L6 H8) bf16, prompt {prompt}, greedy, batch 1",
+            "new_tokens": new_tokens, "tok_per_s_incremental": round(new_tokens / t_inc, 1),
+            "tok_per_s_full_recompute": round(ref_tokens / t_ref, 1),
+            "same_tokens": bool(torch.equal(out[:, :prompt + ref_tokens], ref)),
+            "timing": "wall clock around the whole loop, synchronised"}
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "hbm_traffic_config2.md")
 
@@ -301,6 +341,7 @@ def main(argv=None):
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
     ap.add_argument("--no-pool", action="store_true", help="skip the interference-pool leg")
+    ap.add_argument("--no-generation", action="store_true", help="skip the generation leg")
     ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv"], default=None,
                     help="counter-collection mode: launch only this kernel --profile-reps times, "
                          "plus a plain device copy of --copy-mib MiB (the scale reference for "
@@ -424,6 +465,11 @@ def main(argv=None):
         result["pool"] = bench_pool(dev)
         print(f"[bench] pool fwd {result['pool']['fwd']['us']} us, bwd "
               f"{result['pool']['bwd']['us']} us", file=sys.stderr, flush=True)
+    if not args.no_generation:
+        result["generation"] = bench_generation(dev)
+        g = result["generation"]
+        print(f"[bench] generation {g['tok_per_s_incremental']} tok/s incremental, "
+              f"{g['tok_per_s_full_recompute']} tok/s full recompute", file=sys.stderr, flush=True)
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle sample ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(w, sets[0][0])

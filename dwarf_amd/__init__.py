@@ -11,10 +11,11 @@ from .api import (dsqg_attention, dsqg_attention_qkv, dsqg_attention_v2, dsqg_at
                   dsqg_attention_backend, dsqg_attention_with_lse, dsqg_decode_step,
                   causal_mean_pool_gate, DSQGRingCache)
 from .modules import DSQGAttentionV3, DSQGAttentionQW, DSQGAttentionN_Fused, DSQGBlock, FFN
+from .generation import CondMTransformer, FullAttentionBlock, FullCausalAttention
 
 __all__ = ["ALL_OFFSETS", "OFFSETS_V3", "OFFSETS_J46", "OFFSETS_J47", "dsqg_attention",
            "dsqg_attention_qkv",
            "dsqg_attention_v2", "dsqg_attention_v3", "dsqg_attention_backend",
            "dsqg_attention_with_lse", "dsqg_decode_step", "causal_mean_pool_gate",
            "DSQGRingCache", "DSQGAttentionV3", "DSQGAttentionQW", "DSQGAttentionN_Fused",
-           "DSQGBlock", "FFN"]
+           "DSQGBlock", "FFN", "CondMTransformer", "FullAttentionBlock", "FullCausalAttention"]
