@@ -111,7 +111,6 @@ struct TensorRows {
   int dt;
 };
 
-template <int RPL>
 __device__ __forceinline__ TensorRows rows_of(const void* base, long long sb, long long sn, int dt,
                                               const PoolParams& p, const PoolLane& q) {
   const long long es = dt == DSQG_F32 ? 4 : 2;
@@ -243,7 +242,7 @@ template <int RPL, bool BWD>
 __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const TensorRows tx = rows_of<RPL>(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
   float ax[kCpl], ap[kCpl];
 #pragma unroll
   for (int e = 0; e < kCpl; ++e) ax[e] = ap[e] = 0.f;
@@ -255,8 +254,8 @@ __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
     for (int e = 0; e < kCpl; ++e) ax[e] += v[e];
   }
   if constexpr (BWD) {
-    const TensorRows tg = rows_of<RPL>(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
-    const TensorRows ty = rows_of<RPL>(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
+    const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+    const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {
       float gv[kCpl], yv[kCpl];
@@ -281,8 +280,8 @@ template <int RPL>
 __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const TensorRows tx = rows_of<RPL>(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
-  const TensorRows tg = rows_of<RPL>(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
   float x[RPL][kCpl], s[RPL][kCpl];
   float run[kCpl];
 #pragma unroll
@@ -304,7 +303,7 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
   rl_exclusive_scan<false>(run, sW);
 #pragma unroll
   for (int e = 0; e < kCpl; ++e) run[e] += carry[e];
-  const TensorRows to = rows_of<RPL>(p.out, p.os_b, p.os_n, p.odt, p, q);
+  const TensorRows to = rows_of(p.out, p.os_b, p.os_n, p.odt, p, q);
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     const int n = q.row0 + r;
@@ -324,9 +323,9 @@ template <int RPL>
 __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const TensorRows tx = rows_of<RPL>(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
-  const TensorRows tg = rows_of<RPL>(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
-  const TensorRows ty = rows_of<RPL>(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
+  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+  const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
   float x[RPL][kCpl], s[RPL][kCpl], y[RPL][kCpl];
   float runx[kCpl], runp[kCpl];
 #pragma unroll
@@ -359,8 +358,8 @@ __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) 
     runx[e] += cx[e];
     runp[e] += cp[e];
   }
-  const TensorRows tdg = rows_of<RPL>(p.dg ? p.dg : p.x, p.dgs_b, p.dgs_n, p.gdt, p, q);
-  const TensorRows tdx = rows_of<RPL>(p.dx ? p.dx : p.x, p.dxs_b, p.dxs_n, p.xdt, p, q);
+  const TensorRows tdg = rows_of(p.dg ? p.dg : p.x, p.dgs_b, p.dgs_n, p.gdt, p, q);
+  const TensorRows tdx = rows_of(p.dx ? p.dx : p.x, p.dxs_b, p.dxs_n, p.xdt, p, q);
   // dgate_pre on the way down the rows (prefix sums of x) ...
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
@@ -399,8 +398,7 @@ struct PoolPlan {
 // 64 channels per workgroup; rows per lane: the most (4, 2, 1) that still gives at least 1024
 // workgroups.  (The backward scan at 4 rows is held to 128 VGPRs, four workgroups per CU, at
 // the cost of a few spilled registers: 60 us instead of 65 at [8, 2048, 768] bf16.)
-PoolPlan pool_plan(int B, int N, int C, bool bwd) {
-  (void)bwd;
+PoolPlan pool_plan(int B, int N, int C) {
   PoolPlan pl;
   pl.ctiles = (C + kPoolCh - 1) / kPoolCh;
   for (int rpl = 4; rpl >= 1; rpl >>= 1) {
@@ -437,7 +435,7 @@ int pool_shape_ok(int B, int N, int C) {
 }
 
 size_t pool_workspace(int B, int N, int C, bool bwd) {
-  const PoolPlan pl = pool_plan(B, N, C, bwd);
+  const PoolPlan pl = pool_plan(B, N, C);
   const size_t one = align256_p(sizeof(float) * (size_t)B * pl.nchunks * C);
   return bwd ? 2 * one : one;
 }
@@ -455,7 +453,7 @@ void launch_pool_bwd(const PoolParams& p, unsigned grid, hipStream_t st) {
 }
 
 int run_pool(PoolParams& p, bool bwd, void* ws, size_t ws_bytes, hipStream_t st) {
-  const PoolPlan pl = pool_plan(p.B, p.N, p.C, bwd);
+  const PoolPlan pl = pool_plan(p.B, p.N, p.C);
   if (pl.grid == 0) return DSQG_OK;
   if (pl.grid > 0x7fffffffll) return DSQG_EUNSUPPORTED;
   const size_t one = align256_p(sizeof(float) * (size_t)p.B * pl.nchunks * p.C);
