@@ -197,13 +197,20 @@ class CondMTransformer(nn.Module):
         for block, c in zip(self.blocks, cache.blocks):
             x = block.prefill(x, c)
         cache.pos.fill_(N)
+        cache.n = N
         return self.out(self.norm(x))
 
     @torch.no_grad()
     def step(self, idx_t: Tensor, cache: "GenerationCache") -> Tensor:
         """Logits [B, V] of one new token per sequence (idx_t [B]) at the cache's position.
         Shapes are fixed and positions live on the device, so a step can be captured in a HIP
-        graph and replayed for every further token."""
+        graph and replayed for every further token.  The position must stay inside the position
+        table and the full-attention cache (checked on the host, from the cache's host-side
+        count, before anything is launched)."""
+        if not cache.n < self.seq_len:
+            raise ValueError(f"position {cache.n} is past the position table ({self.seq_len} "
+                             "tokens); continue with forward() on the last seq_len tokens")
+        cache.n += 1
         x = self.embedding(idx_t) + self.pos_embed(cache.pos)
         for block, c in zip(self.blocks, cache.blocks):
             x = block.step(x, c)
@@ -243,6 +250,7 @@ class CondMTransformer(nn.Module):
             elif graph is not None:
                 tok_in.copy_(nxt)
                 graph.replay()
+                cache.n += 1  # the replayed step advanced the device positions
                 logits = logits_out
             else:
                 # The first step runs eagerly on the capture stream (warming up every kernel and
@@ -260,7 +268,7 @@ class CondMTransformer(nn.Module):
                     tok_in.copy_(nxt)
                     graph = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(graph, stream=side):
-                        logits_out = self.step(tok_in, cache)
+                        logits_out = self.step(tok_in, cache)  # counts this token on the host
                     graph.replay()
                     logits = logits_out
                 cur.wait_stream(side)
@@ -269,11 +277,13 @@ class CondMTransformer(nn.Module):
 
 
 class GenerationCache:
-    """The caches of one generation: ``blocks[i]`` for block i, ``pos`` the next position."""
+    """The caches of one generation: ``blocks[i]`` for block i, ``pos`` the next position (on
+    the device, read by the kernels) and ``n`` the same count on the host."""
 
     def __init__(self, blocks: List, pos: Tensor):
         self.blocks = blocks
         self.pos = pos
+        self.n = 0
 
 
 def _sample(logits: Tensor, temperature: float, top_p: float,

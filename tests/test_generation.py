@@ -84,6 +84,14 @@ def test_prefill_then_steps_equal_forward_logits(gpu_device):
     got = torch.stack(steps, dim=1)
     err = (got - full[:, N0:]).abs().max().item()
     assert err <= 1e-4 * scale, f"step logits err {err:.3g} vs scale {scale:.3g}"
+    # Past the position table the step refuses on the host, before launching anything.
+    small = _model(gpu_device, seq_len=64)
+    with torch.no_grad():
+        c2 = small.new_cache(1)
+        small.prefill(ids[:1, :63], c2)
+        small.step(ids[:1, 63], c2)
+        with pytest.raises(ValueError):
+            small.step(ids[:1, 64], c2)
 
 
 def _reference_generate(m, ids, max_new):
