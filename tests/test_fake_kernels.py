@@ -1,0 +1,72 @@
+"""The custom ops' fake (meta) implementations, as torch.compile / export trace them: shapes,
+dtypes and output layouts under FakeTensorMode (no kernel runs; the op-level checks need no
+GPU), and the autograd formulas that call the backward ops (marked gpu: the autograd engine
+initialises the device)."""
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+import dwarf_amd
+from dwarf_amd import ops
+from dwarf_amd.offsets import OFFSETS_V3
+
+B, H, N, D, J = 2, 4, 128, 64, len(OFFSETS_V3)
+
+
+@pytest.fixture
+def fake():
+    with FakeTensorMode(allow_non_fake_inputs=False) as mode:
+        yield mode
+
+
+def _t(*shape, dtype=torch.bfloat16, grad=False):
+    return torch.empty(*shape, dtype=dtype, device="cuda", requires_grad=grad)
+
+
+def test_forward_and_backward_ops(fake):
+    q = _t(B, H, N, D)
+    pb = _t(J, H, dtype=torch.float32)
+    out, lse = ops.dsqg_fwd(q, q, q, pb, None, None, None, list(OFFSETS_V3))
+    assert out.shape == (B, H, N, D) and out.dtype == torch.bfloat16
+    assert out.stride() == (N * H * D, D, H * D, 1)  # token-major storage
+    assert lse.shape == (B, H, N) and lse.dtype == torch.float32
+    grads = ops.dsqg_bwd(q, q, q, q, lse, pb, None, None, None, list(OFFSETS_V3), False, False,
+                         True)
+    assert [tuple(g.shape) for g in grads] == [(B, H, N, D)] * 3 + [(J, H), (0,), (0,), (H,)]
+    qkv = _t(B, N, 3 * H * D)
+    out, lse = ops.dsqg_fwd_qkv(qkv, H, pb, None, None, None, list(OFFSETS_V3))
+    assert out.shape == (B, H, N, D) and lse.shape == (B, H, N)
+    dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv(qkv, H, q, lse, pb, None, None, None,
+                                              list(OFFSETS_V3), True, True, False)
+    assert dqkv.shape == qkv.shape and dse.shape == (J, D) and dg.shape == (H, J)
+
+
+def test_decode_and_pool_ops(fake):
+    q = _t(B, H, D)
+    ring = _t(B, H, 1537, D)
+    pos = torch.empty(B, dtype=torch.int64, device="cuda")
+    pb = _t(J, H, dtype=torch.float32)
+    o = ops.dsqg_decode(q, q, q, ring, ring, pos, pb, None, None, None, list(OFFSETS_V3))
+    assert o.shape == (B, H, D) and o.dtype == torch.bfloat16
+    x = _t(B, N, 32, dtype=torch.float32)
+    g = _t(B, N, 32, dtype=torch.float16)
+    y = ops.pool_gate_fwd(x, g)
+    assert y.shape == (B, N, 32) and y.dtype == torch.float32  # promoted, as in the reference
+    dx, dg = ops.pool_gate_bwd(x, g, y, True, False)
+    assert dx.shape == x.shape and dx.dtype == x.dtype and dg.numel() == 0
+
+
+@pytest.mark.gpu
+def test_autograd_through_fake_tensors(gpu_device, fake):
+    # The autograd engine sets up the device's streams, so this part needs a visible GPU.
+    q, k, v = (_t(B, H, N, D, grad=True) for _ in range(3))
+    pb = _t(J, H, dtype=torch.float32, grad=True)
+    se = _t(J, D, dtype=torch.float32, grad=True)
+    out = dwarf_amd.dsqg_attention_v3(q, k, v, pb, se)
+    out.sum().backward()
+    assert q.grad.shape == q.shape and pb.grad.shape == pb.shape and se.grad.shape == se.shape
+    x = _t(B, N, 64, grad=True)
+    g = _t(B, N, 64, grad=True)
+    dwarf_amd.causal_mean_pool_gate(x, g).sum().backward()
+    assert x.grad.shape == x.shape and g.grad.dtype == g.dtype
