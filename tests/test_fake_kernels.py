@@ -70,3 +70,29 @@ def test_autograd_through_fake_tensors(gpu_device, fake):
     g = _t(B, N, 64, grad=True)
     dwarf_amd.causal_mean_pool_gate(x, g).sum().backward()
     assert x.grad.shape == x.shape and g.grad.dtype == g.dtype
+
+
+@pytest.mark.gpu
+def test_compiled_graph_matches_eager(gpu_device):
+    """A whole-graph capture (torch.compile, aot_eager backend: no generated kernels) of the
+    attention and the pool, forward and backward, gives the eager results bit for bit."""
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(B, H, N, D, generator=g).to(gpu_device, torch.bfloat16) for _ in range(3))
+    pb = torch.randn(J, H, generator=g).to(gpu_device)
+    x = torch.randn(B, N, 64, generator=g).to(gpu_device)
+    gp = torch.randn(B, N, 64, generator=g).to(gpu_device)
+
+    def fn(q, k, v, pb, x, gp):
+        return (dwarf_amd.dsqg_attention_v3(q, k, v, pb, None).float().square().sum()
+                + dwarf_amd.causal_mean_pool_gate(x, gp).square().sum())
+
+    def run(f):
+        ins = [t.clone().requires_grad_(True) for t in (q, k, v, pb, x, gp)]
+        loss = f(*ins)
+        loss.backward()
+        return [loss.detach()] + [t.grad for t in ins]
+
+    eager = run(fn)
+    compiled = run(torch.compile(fn, backend="aot_eager", fullgraph=True))
+    for a, b in zip(eager, compiled):
+        assert torch.equal(a, b)
