@@ -42,22 +42,18 @@ bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
          rmin >= D && span < (1LL << 31);
 }
 
-void bwd_plan(BwdParams& p, int D, int dtype, bool se_grad) {
+void bwd_plan(BwdParams& p, int D, int dtype) {
   const bool mfma = bwd_mfma_supported(p, D, dtype);
   const int QPB = mfma ? 64 : kBlock / (D / 8);  // dq rows per tile
   const int KPB = mfma ? 64 : kBlock / (D / 8);  // dk/dv rows per workgroup
   p.n_tiles = (p.N + QPB - 1) / QPB;
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
-  const long long work = (long long)p.B * p.H * p.n_tiles;
   // One tile per workgroup: the partial rows (J floats, and J x D for dscale_embed) are small next
   // to a tile's loads, and the MFMA kernels' single-tile form keeps no per-lane addresses across
-  // tiles (a tile loop costs them a third of their registers).
-  (void)se_grad;
-  int tpb = 1;
-  if (tpb < 1) tpb = 1;
-  if (tpb > p.n_tiles) tpb = p.n_tiles > 0 ? p.n_tiles : 1;
-  p.tiles_per_block = tpb;
-  p.n_chunks = p.n_tiles > 0 ? (p.n_tiles + tpb - 1) / tpb : 0;
+  // tiles (a tile loop costs them a third of their registers; with scale_embed two tiles per
+  // workgroup spilled 116 registers).
+  p.tiles_per_block = 1;
+  p.n_chunks = p.n_tiles;
 }
 
 hipError_t launch_bwd_reduce_se_stage(const ReduceParams& r, hipStream_t st) {
