@@ -10,7 +10,7 @@ import torch
 
 import dwarf_amd
 from dwarf_amd import ops
-from dwarf_amd.offsets import OFFSETS_V3
+from dwarf_amd.offsets import OFFSETS_J46, OFFSETS_J47, OFFSETS_V3
 from dwarf_amd.workloads import DECODE, make_decode_inputs
 from oracle import decode_step, dsqg_forward
 
@@ -137,3 +137,29 @@ def test_decode_pos_next_and_graph_replay(gpu_device):
         assert err <= 2e-2 * max(1.0, scale)
         assert torch.equal(pos_b.cpu(), pos + 1)
     assert torch.equal(d["k_ring"].cpu(), k_ref) and torch.equal(d["v_ring"].cpu(), v_ref)
+
+
+@pytest.mark.parametrize("offsets,p", [(OFFSETS_J46, 3100), (OFFSETS_J47, 4095),
+                                       ((0, 1, 2, 5, 9, 100), 150), ((0,), 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_other_offset_tables(gpu_device, offsets, p, dtype):
+    """The 46- and 47-offset tables (rings of 3073 and 4097 slots), a short irregular table and
+    the lone delta = 0: the step equals row p of the full-sequence forward."""
+    B, H, D = 2, 2, 64
+    J = len(offsets)
+    g = torch.Generator().manual_seed(p + J)
+    qs, ks, vs = (torch.randn(B, H, p + 1, D, generator=g).to(dtype) for _ in range(3))
+    pb = torch.randn(J, H, generator=g) * 0.5
+    cache = dwarf_amd.DSQGRingCache(B, H, D, offsets, dtype=dtype, device=gpu_device)
+    cache.k_ring.fill_(float("nan"))
+    cache.v_ring.fill_(float("nan"))
+    cache.prefill(ks[:, :, :p].to(gpu_device), vs[:, :, :p].to(gpu_device))
+    out = cache.step(qs[:, :, p].to(gpu_device), ks[:, :, p].to(gpu_device),
+                     vs[:, :, p].to(gpu_device), pb.to(gpu_device)).cpu()
+    cd = torch.float64 if dtype == torch.float32 else torch.float32
+    ref = dsqg_forward(qs.to(cd), ks.to(cd), vs.to(cd), pb.to(cd), None, list(offsets))[:, :, p]
+    err, scale = _err(out, ref)
+    bound = 1e-5 * scale if dtype == torch.float32 else 2e-2 * max(1.0, scale)
+    _say(f"J={J} p={p} {dtype}: err {err:.3e} bound {bound:.3e}")
+    assert torch.isfinite(out).all()
+    assert err <= bound
