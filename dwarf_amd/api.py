@@ -71,8 +71,8 @@ def dsqg_attention(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
     def f32(t):
         return None if t is None else t.float()
 
-    out, _ = ops.dsqg_fwd(q, k, v, pos_bias.float(), f32(scale_embed), f32(score_gain),
-                          f32(if_gain), list(offs))
+    args = (q, k, v, pos_bias.float(), f32(scale_embed), f32(score_gain), f32(if_gain), list(offs))
+    out, _ = ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args)
     return out if out.dtype == orig else out.to(orig)
 
 
@@ -97,8 +97,9 @@ def dsqg_attention_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor,
     def f32(t):
         return None if t is None else t.float()
 
-    out, _ = ops.dsqg_fwd_qkv(qkv, num_heads, pos_bias.float(), f32(scale_embed),
-                              f32(score_gain), f32(if_gain), list(offs))
+    args = (qkv, num_heads, pos_bias.float(), f32(scale_embed), f32(score_gain), f32(if_gain),
+            list(offs))
+    out, _ = ops.dsqg_fwd_qkv(*args) if ops.traced(qkv) else ops.AttentionQkvFn.apply(*args)
     return out if out.dtype == orig else out.to(orig)
 
 
@@ -162,7 +163,9 @@ def causal_mean_pool_gate(x: Tensor, gate_pre: Tensor) -> Tensor:
     assert gate_pre.shape == x.shape, (f"gate_pre must match x {tuple(x.shape)}, "
                                        f"got {tuple(gate_pre.shape)}")
     assert x.shape[2] % 8 == 0, f"channel count {x.shape[2]} must be a multiple of 8"
-    return ops.pool_gate_fwd(x, gate_pre)
+    if ops.traced(x, gate_pre):
+        return ops.pool_gate_fwd(x, gate_pre)
+    return ops.PoolGateFn.apply(x, gate_pre)
 
 
 class DSQGRingCache:

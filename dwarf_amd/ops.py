@@ -249,15 +249,20 @@ def _setup_context(ctx, inputs, output):
     ctx.mark_non_differentiable(lse)
 
 
-def _backward(ctx, dout, _dlse):
+def _backward(ctx, dout, _dlse, direct: bool = False):
     q, k, v, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_dse = bool(need[4]) and scale_embed is not None
     need_dg = bool(need[5]) and score_gain is not None
     need_da = bool(need[6]) and if_gain is not None
-    dq, dk, dv, dpb, dse, dg, da = dsqg_bwd(
-        q, k, v, dout.to(q.dtype), lse, pos_bias, scale_embed, score_gain, if_gain,
-        ctx.offsets, need_dse, need_dg, need_da)
+    args = (q, k, v, dout.to(q.dtype), lse, pos_bias, scale_embed, score_gain, if_gain,
+            ctx.offsets, need_dse, need_dg, need_da)
+    if direct:
+        launch = BwdLaunch(*args)
+        launch.run()
+        dq, dk, dv, dpb, dse, dg, da = launch.outputs()
+    else:
+        dq, dk, dv, dpb, dse, dg, da = dsqg_bwd(*args)
     return (dq, dk, dv, dpb.to(pos_bias.dtype),
             dse.to(scale_embed.dtype) if need_dse else None,
             dg.to(score_gain.dtype) if need_dg else None,
@@ -276,15 +281,16 @@ def _setup_context_qkv(ctx, inputs, output):
     ctx.mark_non_differentiable(lse)
 
 
-def _backward_qkv(ctx, dout, _dlse):
+def _backward_qkv(ctx, dout, _dlse, direct: bool = False):
     qkv, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_dse = bool(need[3]) and scale_embed is not None
     need_dg = bool(need[4]) and score_gain is not None
     need_da = bool(need[5]) and if_gain is not None
-    dqkv, dpb, dse, dg, da = dsqg_bwd_qkv(qkv, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias,
-                                          scale_embed, score_gain, if_gain, ctx.offsets,
-                                          need_dse, need_dg, need_da)
+    args = (qkv, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias, scale_embed, score_gain,
+            if_gain, ctx.offsets, need_dse, need_dg, need_da)
+    bwd = _bwd_qkv_impl if direct else dsqg_bwd_qkv
+    dqkv, dpb, dse, dg, da = bwd(*args)
     return (dqkv, None, dpb.to(pos_bias.dtype),
             dse.to(scale_embed.dtype) if need_dse else None,
             dg.to(score_gain.dtype) if need_dg else None,
@@ -298,6 +304,12 @@ def dsqg_bwd_qkv(qkv: Tensor, num_heads: int, dout: Tensor, lse: Tensor, pos_bia
                  need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(dqkv [B,N,3*H*HD], dpos_bias, dscale_embed, dscore_gain, dif_gain): dq, dk, dv are
     written straight into the head views of one gradient buffer."""
+    return _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain,
+                         offsets, need_dse, need_dg, need_da)
+
+
+def _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
+                  need_dse, need_dg, need_da):
     q, k, v = split_qkv(qkv, num_heads)
     dqkv = torch.empty_like(qkv, memory_format=torch.contiguous_format)
     launch = BwdLaunch(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
@@ -322,6 +334,50 @@ def _(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, off
 
 torch.library.register_autograd("dwarf::dsqg_fwd_qkv", _backward_qkv,
                                 setup_context=_setup_context_qkv)
+
+
+# Eager autograd over the same launch objects: the custom ops above are what traced code
+# (torch.compile, export, fake tensors) sees; outside tracing the public functions take these
+# Functions, which skip the custom-op dispatch (about 100 us of host time per forward +
+# backward, measured on the MI355X host, where the kernels themselves take a few tens of us
+# at small shapes).  Same kernels, same results.
+
+def traced(*tensors) -> bool:
+    """True under torch.compile / export or for fake or meta tensors: use the custom ops."""
+    if torch.compiler.is_compiling():
+        return True
+    from torch._subclasses.fake_tensor import FakeTensor
+    return any(isinstance(t, FakeTensor) or (t is not None and t.device.type == "meta")
+               for t in tensors)
+
+
+class AttentionFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
+        launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
+        launch.run()
+        _setup_context(ctx, (q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets),
+                       (launch.out, launch.lse))
+        return launch.out, launch.lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        return _backward(ctx, dout, dlse, direct=True)
+
+
+class AttentionQkvFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets):
+        q, k, v = split_qkv(qkv, num_heads)
+        launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
+        launch.run()
+        _setup_context_qkv(ctx, (qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain,
+                                 offsets), (launch.out, launch.lse))
+        return launch.out, launch.lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        return _backward_qkv(ctx, dout, dlse, direct=True)
 
 
 # ------------------------------------------------------------------------------------------
@@ -506,3 +562,24 @@ def _pool_backward(ctx, dout):
 
 torch.library.register_autograd("dwarf::pool_gate_fwd", _pool_backward,
                                 setup_context=_pool_setup_context)
+
+
+class PoolGateFn(torch.autograd.Function):
+    """Eager autograd of the pool over the launch objects (see AttentionFn)."""
+
+    @staticmethod
+    def forward(ctx, x, gate_pre):
+        launch = PoolLaunch(x, gate_pre)
+        launch.run()
+        ctx.save_for_backward(x, gate_pre)
+        return launch.out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, gate_pre = ctx.saved_tensors
+        need_dx, need_dg = bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1])
+        if not (need_dx or need_dg):
+            return None, None
+        launch = PoolLaunch(x, gate_pre, dout, need_dx, need_dg)
+        launch.run()
+        return (launch.dx if need_dx else None), (launch.dgate if need_dg else None)
