@@ -8,6 +8,7 @@ if the library is missing, every entry point raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from pathlib import Path
 
@@ -153,6 +154,13 @@ def supported_head_dims() -> list[int]:
 
 
 def make_shape(dtype_code: int, B: int, H: int, N: int, D: int, offsets) -> Shape:
+    """A dsqg_shape block: a copy of a cached one (filling the 64-entry offset table from
+    Python costs more than the copy)."""
+    return Shape.from_buffer_copy(_shape_cached(dtype_code, B, H, N, D, tuple(int(o) for o in offsets)))
+
+
+@functools.lru_cache(maxsize=256)
+def _shape_cached(dtype_code: int, B: int, H: int, N: int, D: int, offsets: tuple) -> Shape:
     offs = list(offsets)
     if not 1 <= len(offs) <= MAX_OFFSETS:
         raise ValueError(f"offset table must have 1..{MAX_OFFSETS} entries, got {len(offs)}")

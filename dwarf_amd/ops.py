@@ -53,7 +53,9 @@ def _rows_ready(t: Tensor) -> Tensor:
 
 
 def _param(t: Optional[Tensor]) -> Optional[Tensor]:
-    return None if t is None else t.detach().to(torch.float32).contiguous()
+    if t is None or (t.dtype == torch.float32 and t.is_contiguous()):
+        return t  # only its pointer is passed on; the launch keeps a reference
+    return t.detach().to(torch.float32).contiguous()
 
 
 def _strides(t: Tensor):
