@@ -14,6 +14,7 @@ Reference counterparts: _DSQGFnV3.forward / .backward (kernels/dsqg_attention_v3
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import List, Optional, Tuple
 
 import torch
@@ -463,11 +464,17 @@ def _pool_strides(t: Tensor):
     return (ctypes.c_int64 * 2)(t.stride(0), t.stride(1))
 
 
-def _pool_workspace(lib, B, N, C, backward: bool, dev) -> Tensor:
+@functools.lru_cache(maxsize=256)
+def _pool_workspace_bytes(B: int, N: int, C: int, backward: bool) -> int:
     n = ctypes.c_size_t(0)
-    _lib.check(lib.dsqg_pool_gate_workspace_size(B, N, C, int(backward), ctypes.byref(n)),
+    _lib.check(_lib.load().dsqg_pool_gate_workspace_size(B, N, C, int(backward), ctypes.byref(n)),
                "dsqg_pool_gate_workspace_size")
-    return torch.empty((max(int(n.value), 1),), dtype=torch.uint8, device=dev)
+    return int(n.value)
+
+
+def _pool_workspace(lib, B, N, C, backward: bool, dev) -> Tensor:
+    return torch.empty((max(_pool_workspace_bytes(B, N, C, backward), 1),), dtype=torch.uint8,
+                       device=dev)
 
 
 class PoolLaunch:
