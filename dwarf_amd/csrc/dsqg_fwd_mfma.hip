@@ -20,10 +20,11 @@
 //  5. Softmax over each query's J taps in registers: the four lanes of a query column combine
 //     max and sum with two cross-lane steps; lse = max + log(sum); the weights are normalised
 //     (and scaled by the IF gain) before P V.
-//  6. Dense P V: O^T = V^T P^T with v_mfma_f32_16x16x16_bf16.  V^T comes from the row-major LDS
-//     tile through ds_read_tr16_b64; P^T is already in B layout.  Long-range P V on the VALU in
-//     the whole-row layout (each lane adds p * v for its rows' 16-byte chunk, the weights read
-//     from the wave's table); the two parts meet in LDS and leave as 16-byte row stores.
+//  6. P V: O^T = V^T P^T with v_mfma_f32_16x16x16_bf16.  Dense taps: V^T from the row-major
+//     window tile through ds_read_tr16_b64, P^T already in B layout.  Long-range taps: each
+//     tap's 16 V rows (gathered whole-row) are staged in the wave's LDS block and read back the
+//     same way, against a one-hot P^T held by the query's diagonal lane.  The output leaves
+//     through the same block as 16-byte row stores.
 //
 // Semantics: _fwd_v3, kernels/dsqg_attention_v3.py:60-163 (plus score gain and IF gain).
 #include "dsqg_common.hpp"
@@ -44,17 +45,23 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   constexpr int CHW = 16 * CPR / 64;      // chunks per lane of a wave's 16-row block
   static_assert(16 * CPR % 64 == 0, "a wave's 16-row block must split evenly over 64 lanes");
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
+#ifdef DSQG_FWD_PF
+  constexpr int PF = DSQG_FWD_PF;
+#else
   constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
+#endif
   constexpr int TS = 38;                  // row stride of the per-wave T table (dense taps; 2-way reads)
   constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
-  constexpr int XE = 8 * 2 * (D + 4);     // bf16 elements of the output exchange (8 rows x (D+4) floats)
+  constexpr int TR = NSM + (NSM & 1);     // row stride of the long-range score table (distinct banks)
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sV[WIN * RV];
   __shared__ __align__(16) bf16_t sK[WIN * RV];   // dense-window K rows (MFMA A operands)
-  __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : XE];   // wave-private staging block
+  // Wave-private staging block (16 rows x RV): the T table (scale_embed), then each long-range
+  // tap's V rows, then the output rows.
+  __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : 16 * RV];
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
-  __shared__ __align__(16) float sRaw[4][16 * 16];   // per wave: long-range q.k [query][tap]
+  __shared__ __align__(16) float sRaw[4][16 * TR];   // per wave: long-range q.k [query][tap]
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
 
@@ -164,7 +171,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
         d = fmaf(c2, dot8_bf16(qR[u], se, 0.f), d);
       }
       d = group_sum<CPR>(d);
-      if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * 16 + t] = d;
+      if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * TR + t] = d;
     }
   };
 #pragma unroll
@@ -241,7 +248,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     ss[t] = -INFINITY;
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      const float v = sRw[i * 16 + t] + sBias2[j];
+      const float v = sRw[i * TR + t] + sBias2[j];
       ss[t] = (diag && row_ok && n >= dl_s[t]) ? v : -INFINITY;
     }
   }
@@ -278,87 +285,46 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vr + 16 * db), pb, accO[db]);
   }
 
-  // ---- Long-range P V on the VALU, whole-row layout: o_L[row] += p_t[row] * v_t[row]. ----
-  // The diagonal lanes publish the normalised long-range weights in the wave's table (as bf16
-  // in the low half of each word); every lane then adds p * v for the 16-byte chunk of its rows,
-  // with no per-tap LDS round trip.
-  unsigned* sRwU = reinterpret_cast<unsigned*>(sRw);
-  if (diag) {
-#pragma unroll
-    for (int t = 0; t < NSM; ++t)
-      if (NSC > 0 || t < NS) sRwU[i * 16 + t] = bf16_bits(ss[t] * inv);
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the weights are in the table
-  __builtin_amdgcn_wave_barrier();
-  float oL[CHW][8];
-#pragma unroll
-  for (int u = 0; u < CHW; ++u)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) oL[u][e] = 0.f;
+  // ---- Long-range P V on the MFMA: O^T += V_t^T P_t^T per tap. ----
+  // The tap's 16 V rows (gathered whole-row) are staged in the wave's block in natural row order
+  // and read back transposed (ds_read_tr16_b64) as the A operand; P_t^T is one-hot: only the
+  // diagonal lane of query i holds a weight (the others' ss[t] are exp2(-inf) = 0), at key i.
+  bf16_t* const sSt = sVs[w];
+  const bf16_t* const vtr = sSt + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
 #pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        // The weight as the bf16 pairs (p, 0) and (0, p): one v_dot2 per element multiplies
-        // and accumulates without unpacking the bf16 V pair (p rounded to bf16, as the MFMA
-        // P V of the dense taps rounds it).
-        const unsigned plo = sRwU[rc_row<D>(l, u) * 16 + t];
-        const unsigned phi = plo << 16;
-        const uint4 x = vS[t % PF][u];
-        const unsigned wd[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          oL[u][2 * e] = dot2_bf16(plo, wd[e], oL[u][2 * e]);
-          oL[u][2 * e + 1] = dot2_bf16(phi, wd[e], oL[u][2 * e + 1]);
-        }
-      }
+      for (int u = 0; u < CHW; ++u) st16(sSt + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, vS[t % PF][u]);
       if (t + PF < NS) {
         const int r0 = n0w - dl_s[t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) vS[t % PF][u] = bload16(rV, r0 * vsn + vlane[u]);
       }
-      // Pin this tap's multiply-adds here: left free, the compiler defers every tap's
-      // accumulation behind all the loads and spills (14 registers at four workgroups per CU).
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
+      __builtin_amdgcn_wave_barrier();
+      // The weight rounded to bf16, as the dense band's P V rounds its weights.
+      const s16x4_t pb = onehot_bf16x4(ss[t] * inv, i & 3);
 #pragma unroll
-      for (int u = 0; u < CHW; ++u)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(oL[u][e]));
+      for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vtr + 16 * db), pb, accO[db]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // ---- out = O_dense (MFMA layout) + o_L (row layout), stored as whole rows. ----
-  // Two rounds of 8 rows through the wave's free staging block (8 x (D+4) floats each): the
-  // MFMA lanes of those rows deposit their values, the row-layout lanes add theirs and store
-  // 16 bytes per lane.
-  float* xb = reinterpret_cast<float*>(sVs[w]);
-  constexpr int XS = D + 4;
+  // ---- out (MFMA layout: lane (i, g) holds query i, d = 16 db + 4 g + 0..3) leaves as whole
+  // rows: the lanes deposit bf16 quads in the wave's block, then 16-byte row pieces are stored.
   bf16_t* outb = static_cast<bf16_t*>(p.out) + b * p.os.b + h * p.os.h;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    if ((i >> 3) == half) {
+  for (int db = 0; db < DB; ++db)
+    *reinterpret_cast<uint2*>(sSt + i * RV + 16 * db + 4 * g) =
+        pack_bf16x4_u2(accO[db][0], accO[db][1], accO[db][2], accO[db][3]);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-        *reinterpret_cast<float4*>(xb + (i & 7) * XS + 16 * db + 4 * g) =
-            make_float4(accO[db][0], accO[db][1], accO[db][2], accO[db][3]);
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int u = 0; u < CHW; ++u) {
-      const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
-      if ((rr >> 3) == half && n0w + rr < N) {
-        const float* src = xb + (rr & 7) * XS + 8 * cc;
-        const float4 lo = *reinterpret_cast<const float4*>(src);
-        const float4 hi = *reinterpret_cast<const float4*>(src + 4);
-        const uint2 a0 = pack_bf16x4_u2(lo.x + oL[u][0], lo.y + oL[u][1], lo.z + oL[u][2], lo.w + oL[u][3]);
-        const uint2 a1 = pack_bf16x4_u2(hi.x + oL[u][4], hi.y + oL[u][5], hi.z + oL[u][6], hi.w + oL[u][7]);
-        st16(outb + (n0w + rr) * p.os.n + 8 * cc, make_uint4(a0.x, a0.y, a1.x, a1.y));
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // this round's reads are done before the next writes
-    __builtin_amdgcn_wave_barrier();
+  for (int u = 0; u < CHW; ++u) {
+    const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+    if (n0w + rr < N)
+      st16(outb + (n0w + rr) * p.os.n + 8 * cc, *reinterpret_cast<const uint4*>(sSt + rr * RV + 8 * cc));
   }
 }
 

@@ -123,13 +123,6 @@ __device__ __forceinline__ s16x4_t onehot_bf16x4(float x, int e) {
   return __builtin_bit_cast(s16x4_t, v);
 }
 
-// Element r (runtime, 0..3) of a 4-vector without dynamic register indexing.
-__device__ __forceinline__ float pick4(f32x4_t v, int r) {
-  const float lo = (r & 1) ? v[1] : v[0];
-  const float hi = (r & 1) ? v[3] : v[2];
-  return (r & 2) ? hi : lo;
-}
-
 // Max / sum over the four lanes {i, i+16, i+32, i+48} that share column i of an MFMA tile.
 // v_permlane16_swap / v_permlane32_swap (gfx950) hand every lane the pair {x[l], x[l^16]}
 // (resp. x[l^32]) without an LDS round trip; the pair is combined in the same order on both
@@ -152,21 +145,5 @@ __device__ __forceinline__ float xor32_pair_max(float x) {
 }
 __device__ __forceinline__ float col_max(float x) { return xor32_pair_max(xor16_pair_max(x)); }
 __device__ __forceinline__ float col_sum(float x) { return xor32_pair_sum(xor16_pair_sum(x)); }
-
-// Rotated diagonals for the long-range taps.  Taps are processed in groups of four; for tap tl
-// (0..3) of a group, MFMA A row rho = 4*gg + rr loads key row sigma = 4*((gg - tl) & 3) + rr of
-// the tap's 16-row block.  The score of query column i then lands in lane group
-// g = (i/4 + tl) & 3, register i & 3, so lane (i, g) owns exactly one tap of each group:
-// tl = (g - i/4) & 3.  Blocks staged in LDS keep the A-row order, so the one-hot P / dS
-// operand of the follow-up transposed product is non-zero in that same lane.
-__device__ __forceinline__ int rot_row(int rho, int tl) { return 4 * (((rho >> 2) - tl) & 3) + (rho & 3); }
-__device__ __forceinline__ int rot_tap(int i, int g) { return (g - (i >> 2)) & 3; }
-
-// Element [t][r] of four 4-vectors for runtime t, r (0..3), by selects.
-__device__ __forceinline__ float pick16(const f32x4_t (&v)[4], int t, int r) {
-  const float a = (t & 1) ? pick4(v[1], r) : pick4(v[0], r);
-  const float b = (t & 1) ? pick4(v[3], r) : pick4(v[2], r);
-  return (t & 2) ? b : a;
-}
 
 }  // namespace dsqg
