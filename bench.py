@@ -247,12 +247,18 @@ def bench_generation(dev, prompt=1024, new_tokens=64, ref_tokens=16):
     m = CondMTransformer(32000, 256, 6, 8, 1024, 2048, dropout=0.0).to(dev, torch.bfloat16).eval()
     ids = torch.randint(0, 32000, (1, prompt), device=dev)
 
-    def timed(fn):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        out = fn()
-        torch.cuda.synchronize()
-        return out, time.perf_counter() - t0
+    def timed(fn, reps=3):
+        # Both loops are host-bound at batch 1 (the reference's most of all: ~300 launches per
+        # token), so the best of a few repetitions is kept against transient host contention.
+        best = None
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = fn()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        return out, best
 
     m.generate(ids[:, :64], 4, temperature=0.0)  # warm-up
     out, t_inc = timed(lambda: m.generate(ids, new_tokens, temperature=0.0))
@@ -271,7 +277,7 @@ def bench_generation(dev, prompt=1024, new_tokens=64, ref_tokens=16):
             "new_tokens": new_tokens, "tok_per_s_incremental": round(new_tokens / t_inc, 1),
             "tok_per_s_full_recompute": round(ref_tokens / t_ref, 1),
             "same_tokens": bool(torch.equal(out[:, :prompt + ref_tokens], ref)),
-            "timing": "wall clock around the whole loop, synchronised"}
+            "timing": "wall clock around the whole loop, synchronised, best of 3"}
 
 
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
