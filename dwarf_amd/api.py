@@ -50,6 +50,17 @@ def _check_shapes(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
         assert tuple(if_gain.shape) == (H,), f"if_gain must be {(H,)}, got {tuple(if_gain.shape)}"
 
 
+def _f32(t: Optional[Tensor]) -> Optional[Tensor]:
+    return None if t is None else t.float()
+
+
+def _compute_dtype(q: Tensor, k: Tensor, v: Tensor):
+    """q, k, v in the dtype the kernels compute in: q's if float32 or bfloat16, else bfloat16."""
+    if q.dtype not in (torch.float32, torch.bfloat16):
+        return q.bfloat16(), k.bfloat16(), v.bfloat16()
+    return q, k.to(q.dtype), v.to(q.dtype)
+
+
 def dsqg_attention(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
                    scale_embed: Optional[Tensor] = None, *,
                    offsets: Optional[Sequence[int]] = None,
@@ -63,15 +74,9 @@ def dsqg_attention(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
     offs = validate(offsets) if offsets is not None else default_offsets(pos_bias.shape[0])
     _check_shapes(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offs)
     orig = q.dtype
-    if orig not in (torch.float32, torch.bfloat16):
-        q, k, v = q.bfloat16(), k.bfloat16(), v.bfloat16()
-    elif k.dtype != orig or v.dtype != orig:
-        k, v = k.to(orig), v.to(orig)
-
-    def f32(t):
-        return None if t is None else t.float()
-
-    args = (q, k, v, pos_bias.float(), f32(scale_embed), f32(score_gain), f32(if_gain), list(offs))
+    q, k, v = _compute_dtype(q, k, v)
+    args = (q, k, v, pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain),
+            list(offs))
     out, _ = ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args)
     return out if out.dtype == orig else out.to(orig)
 
@@ -93,11 +98,7 @@ def dsqg_attention_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor,
     orig = qkv.dtype
     if orig not in (torch.float32, torch.bfloat16):
         qkv = qkv.bfloat16()
-
-    def f32(t):
-        return None if t is None else t.float()
-
-    args = (qkv, num_heads, pos_bias.float(), f32(scale_embed), f32(score_gain), f32(if_gain),
+    args = (qkv, num_heads, pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain),
             list(offs))
     out, _ = ops.dsqg_fwd_qkv(*args) if ops.traced(qkv) else ops.AttentionQkvFn.apply(*args)
     return out if out.dtype == orig else out.to(orig)
@@ -122,15 +123,15 @@ def dsqg_attention_backend(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
 
 def dsqg_attention_with_lse(q, k, v, pos_bias, scale_embed=None, *, offsets=None,
                             score_gain=None, if_gain=None):
-    """(out, lse) in the dtype rules above; lse [B,H,N] fp32 is not differentiable."""
+    """(out, lse): out in the dtype rules above (differentiable), lse [B,H,N] fp32 (not)."""
     offs = validate(offsets) if offsets is not None else default_offsets(pos_bias.shape[0])
     _check_shapes(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offs)
-
-    def f32(t):
-        return None if t is None else t.float()
-
-    return ops.dsqg_fwd(q, k, v, pos_bias.float(), f32(scale_embed), f32(score_gain),
-                        f32(if_gain), list(offs))
+    orig = q.dtype
+    q, k, v = _compute_dtype(q, k, v)
+    args = (q, k, v, pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain),
+            list(offs))
+    out, lse = ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args)
+    return (out if out.dtype == orig else out.to(orig)), lse
 
 
 def dsqg_decode_step(q: Tensor, k_new: Tensor, v_new: Tensor, k_ring: Tensor, v_ring: Tensor,

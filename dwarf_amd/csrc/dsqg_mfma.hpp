@@ -48,17 +48,6 @@ __device__ __forceinline__ uint2 pack_bf16x4_u2(float a, float b, float c, float
 
 __device__ __forceinline__ f32x4_t zero4() { return f32x4_t{0.f, 0.f, 0.f, 0.f}; }
 
-// Bits of x rounded to bf16 (nearest even), in the low half of the word, high half zero.
-__device__ __forceinline__ unsigned bf16_bits(float x) {
-  return (unsigned)__builtin_bit_cast(unsigned short, (__bf16)x);
-}
-
-// acc + a.lo * b.lo + a.hi * b.hi for two packed bf16 pairs (v_dot2_f32_bf16).
-__device__ __forceinline__ float dot2_bf16(unsigned a, unsigned b, float acc) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc, false);
-}
-
 // acc + a . b over eight bf16 pairs (v_dot2_f32_bf16: exact products, fp32 accumulation).
 __device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

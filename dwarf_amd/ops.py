@@ -472,7 +472,7 @@ def _pool_workspace_bytes(B: int, N: int, C: int, backward: bool) -> int:
     return int(n.value)
 
 
-def _pool_workspace(lib, B, N, C, backward: bool, dev) -> Tensor:
+def _pool_workspace(B, N, C, backward: bool, dev) -> Tensor:
     return torch.empty((max(_pool_workspace_bytes(B, N, C, backward), 1),), dtype=torch.uint8,
                        device=dev)
 
@@ -494,7 +494,7 @@ class PoolLaunch:
         x = _pool_ready(x, B, N, C, "x")
         g = _pool_ready(gate_pre, B, N, C, "gate_pre")
         self.backward = dout is not None
-        self.ws = _pool_workspace(self.lib, B, N, C, self.backward, dev)
+        self.ws = _pool_workspace(B, N, C, self.backward, dev)
         if not self.backward:
             self.out = torch.empty((B, N, C), dtype=torch.promote_types(x.dtype, g.dtype),
                                    device=dev)

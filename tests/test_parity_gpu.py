@@ -251,6 +251,23 @@ def test_fp16_inputs_follow_reference_cast(gpu_device):
     check("out(fp16 via bf16)", out.float().cpu(), ref, "bf16")
 
 
+def test_with_lse_follows_the_dtype_rules(gpu_device):
+    """dsqg_attention_with_lse: fp16 inputs are computed in bf16 and out comes back as fp16,
+    lse [B,H,N] fp32 matches the oracle's logsumexp; out is differentiable."""
+    inp = _rand_inputs(1, 2, 300, 64, OFFSETS_V3, torch.float16, seed=5, gains=False)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    q = d["q"].clone().requires_grad_(True)
+    out, lse = dwarf_amd.dsqg_attention_with_lse(q, d["k"], d["v"], d["pos_bias"], d["scale_embed"])
+    assert out.dtype == torch.float16 and lse.dtype == torch.float32 and tuple(lse.shape) == (1, 2, 300)
+    ref, ref_lse = dsqg_forward(inp["q"].bfloat16().float(), inp["k"].bfloat16().float(),
+                                inp["v"].bfloat16().float(), inp["pos_bias"], inp["scale_embed"],
+                                return_lse=True)
+    check("out(with_lse)", out.float().cpu(), ref, "bf16")
+    check("lse(with_lse)", lse.cpu(), ref_lse, "bf16")
+    out.float().sum().backward()
+    assert q.grad is not None and q.grad.dtype == torch.float16
+
+
 def test_v3_with_zero_scale_embed_equals_v2(gpu_device):
     """kernels/dsqg_attention_v3.py:612-628: V3(SE=0) == V2."""
     inp = _rand_inputs(2, 8, 128, 32, OFFSETS_V3, torch.bfloat16, seed=7, se=False, gains=False)
