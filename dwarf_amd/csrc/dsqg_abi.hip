@@ -102,6 +102,7 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   p->qs = to_strides(a->q_stride); p->ks = to_strides(a->k_stride);
   p->vs = to_strides(a->v_stride); p->dos = to_strides(a->dout_stride);
   bwd_plan(*p, s.D, s.dtype);
+  if (s.dtype == DSQG_BF16 && !bwd_mfma_supported(*p, s.D, s.dtype)) return DSQG_EUNSUPPORTED;
   if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;
   if ((long long)s.B * s.H * p->n_tiles_kv > INT_MAX / 2) return DSQG_EINVAL;
   return DSQG_OK;
@@ -117,7 +118,9 @@ const char* dsqg_status_string(int status) {
   switch (status) {
     case DSQG_OK: return "ok";
     case DSQG_EINVAL: return "invalid argument (shape, stride, alignment, pointer or offset table)";
-    case DSQG_EUNSUPPORTED: return "unsupported configuration (no kernel for this head dim)";
+    case DSQG_EUNSUPPORTED:
+      return "unsupported configuration (head dim, more than 48 offsets, or a bf16 table with "
+             "more than 16 offsets beyond the dense window)";
     case DSQG_EHIP: return "HIP launch error";
     case DSQG_EWORKSPACE: return "workspace missing or too small";
     default: return "unknown status";
@@ -155,6 +158,9 @@ int dsqg_fwd(const dsqg_fwd_args* a, dsqg_stream_t stream) {
   p.score_gain = a->score_gain; p.if_gain = a->if_gain;
   p.out = a->out; p.os = to_strides(a->out_stride);
   p.lse = a->lse;
+  // bf16 has one implementation, the MFMA kernel: tables with more long-range taps than it
+  // holds, or slices beyond its 32-bit offsets, are not taken.
+  if (s.dtype == DSQG_BF16 && !fwd_mfma_supported(p, s.D)) return DSQG_EUNSUPPORTED;
   return hip_status(launch_fwd(p, s.dtype, s.D, reinterpret_cast<hipStream_t>(stream)));
 }
 

@@ -150,8 +150,7 @@ static hipError_t launch_bwd_dkdv_dtype(const BwdParams& p, int D, unsigned nb, 
 
 hipError_t launch_bwd_dkdv(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st) {
   if (bwd_mfma_supported(p, D, dtype)) return launch_bwd_dkdv_mfma(p, D, nblocks, st);
-  return dtype == 0 ? launch_bwd_dkdv_dtype<float>(p, D, nblocks, st)
-                    : launch_bwd_dkdv_dtype<bf16_t>(p, D, nblocks, st);
+  return dtype == 0 ? launch_bwd_dkdv_dtype<float>(p, D, nblocks, st) : hipErrorNotSupported;
 }
 
 hipError_t launch_bwd_dkdv_params(const BwdParams& p, const ReduceParams& r, int dtype, int D,

@@ -13,11 +13,16 @@
 //  * Long-range taps: query rows m0w + delta + 0..15, loaded whole-row (D/8 lanes per row: the
 //    vector L1 serves that at close to four times the rate of the MFMA operand order); q.k,
 //    dOut.v and q.se_j are VALU dot products (v_dot2_f32_bf16, DPP sums over the row's lanes)
-//    handed to the diagonal lane (16*(i/4)+i, register i%4) through LDS.  The query / dOut rows
-//    are staged in the wave's rows of the (by then free) window tiles for the transposed reads
-//    of the diagonal update; the LDS then fits four workgroups per CU (three with scale_embed).
+//    handed to the lanes of key column i through LDS.  The query / dOut rows are staged in the
+//    wave's rows of the (by then free) window tiles; each tap's diagonal update is one
+//    v_mfma_f32_16x16x32_bf16 per 16 head dims whose k runs over the 16 staged rows twice, against
+//    a one-hot operand holding the weight as bf16 hi (k = i) and lo (k = 16 + i), so the weight
+//    keeps its fp32 precision.  The LDS fits four workgroups per CU (three with scale_embed).
+//  * The dense band's weights enter their MFMAs as bf16 hi + lo pairs (two products each).
 //  * The q.se_j term of the score (scale_embed) is a [query][tap] table per wave computed on the
-//    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps.
+//    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps, both with se
+//    rounded to bf16 (an error of about 2^-9 |c q.se| in the score, 1e-4 at the reference's
+//    se ~ 0.05; the parameter gradients come from launch 1, which keeps se at fp32 precision).
 // With p.red_blocks > 0 the launch carries that many extra workgroups at the end of the grid,
 // which sum the parameter-gradient partials (dsqg_reduce.hpp) while the dk/dv tiles run.
 // Follows _bwd_dkdv_v3 (kernels/dsqg_attention_v3.py:282-352).
@@ -216,14 +221,19 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
       wk[r] = sGainC[j] * dS;
       wv[r] = a * alpha;
     }
-    const s16x4_t bk = pack_bf16x4(wk[0], wk[1], wk[2], wk[3]);
-    const s16x4_t bv = pack_bf16x4(wv[0], wv[1], wv[2], wv[3]);
+    // The weights as bf16 hi + lo pairs, so the products keep their fp32 precision.
+    s16x4_t bk, bkl, bv, bvl;
+    split_bf16x4(wk[0], wk[1], wk[2], wk[3], bk, bkl);
+    split_bf16x4(wv[0], wv[1], wv[2], wv[3], bv, bvl);
     const bf16_t* qr = sQ + (16 * w + 16 * qb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
     const bf16_t* orr = sO + (16 * w + 16 * qb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      dK[db] = mfma_16x16x16(lds_read_tr16(qr + 16 * db), bk, dK[db]);
-      dV[db] = mfma_16x16x16(lds_read_tr16(orr + 16 * db), bv, dV[db]);
+      const s16x4_t qt = lds_read_tr16(qr + 16 * db), ot = lds_read_tr16(orr + 16 * db);
+      dK[db] = mfma_16x16x16(qt, bk, dK[db]);
+      dK[db] = mfma_16x16x16(qt, bkl, dK[db]);
+      dV[db] = mfma_16x16x16(ot, bv, dV[db]);
+      dV[db] = mfma_16x16x16(ot, bvl, dV[db]);
     }
   }
 
@@ -246,14 +256,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
       }
     }
   }
-  const bool diag = g == (i >> 2);
+  const bool sel_hi = g == (i >> 3), sel_lo = g == 2 + (i >> 3);
   // The wave's long-range query / dOut rows are staged in the window tiles (rows 16w..16w+15),
   // free once every wave's band is done.
   bf16_t* qsw = sQ + w * 16 * RV;
   bf16_t* osw = sO + w * 16 * RV;
   __syncthreads();  // every wave's band reads of sQ / sO are done
-  const bf16_t* qtr = qsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
-  const bf16_t* otr = osw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
@@ -291,16 +299,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
       __builtin_amdgcn_wave_barrier();
       const float2 pr = sPair[w][i];
       const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
-      const bool ok = diag && key_ok && nq < N;
+      const bool ok = key_ok && nq < N;  // every lane of column i: the stacked operand below
       const float uval = pr.y;
       const float alpha = ok ? __builtin_amdgcn_exp2f(pr.x + sBias2[j] - lseq) : 0.f;
       const float dS = a * alpha * (uval - dpq);
-      const s16x4_t bk = onehot_bf16x4(sGainC[j] * dS, i & 3);
-      const s16x4_t bv = onehot_bf16x4(a * alpha, i & 3);
+      const bf16x8_t bk = onehot_hilo_bf16x8(sGainC[j] * dS, sel_hi, sel_lo, i & 7);
+      const bf16x8_t bv = onehot_hilo_bf16x8(a * alpha, sel_hi, sel_lo, i & 7);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        dK[db] = mfma_16x16x16(lds_read_tr16(qtr + 16 * db), bk, dK[db]);
-        dV[db] = mfma_16x16x16(lds_read_tr16(otr + 16 * db), bv, dV[db]);
+        dK[db] = mfma_16x16x32(lds_read_tr16_stacked(qsw, RV, i, g, 16 * db), bk, dK[db]);
+        dV[db] = mfma_16x16x32(lds_read_tr16_stacked(osw, RV, i, g, 16 * db), bv, dV[db]);
       }
     }
   }

@@ -246,8 +246,7 @@ static hipError_t launch_bwd_dq_dtype(const BwdParams& p, int D, unsigned nb, hi
 
 hipError_t launch_bwd_dq(const BwdParams& p, int dtype, int D, unsigned nblocks, hipStream_t st) {
   if (bwd_mfma_supported(p, D, dtype)) return launch_bwd_dq_mfma(p, D, nblocks, st);
-  return dtype == 0 ? launch_bwd_dq_dtype<float>(p, D, nblocks, st)
-                    : launch_bwd_dq_dtype<bf16_t>(p, D, nblocks, st);
+  return dtype == 0 ? launch_bwd_dq_dtype<float>(p, D, nblocks, st) : hipErrorNotSupported;
 }
 
 }  // namespace dsqg

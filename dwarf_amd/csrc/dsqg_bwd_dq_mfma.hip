@@ -18,7 +18,11 @@
 // the tile's 64 queries, its [D x J] output tiles split over the four waves).
 // With scale_embed the q.se_j term of the dense taps is an MFMA (SE Q^T) filed in a per-wave
 // [query][tap] table that shares the wave's staging block; for the long-range taps it is a VALU
-// dot product folded into the score, like q.k.
+// dot product folded into the score, like q.k.  scale_embed is staged as two bf16 planes
+// (hi = bf16(se), lo = bf16(se - hi)), and every weight that enters an MFMA (the dense band's
+// and the one-hot long-range X / Y weights, dS in dse and in SE^T dS^T) is split the same way,
+// so these products keep fp32 precision as in the reference (kernels/dsqg_attention_v3.py:
+// 257-271 sums dq and dse in fp32).
 //
 // Follows _compute_D_v3 + _bwd_dq_v3 (kernels/dsqg_attention_v3.py:170-275), except that D' is
 // computed from the fp32 weights and the parameter gradients avoid atomics.
@@ -57,7 +61,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
   // T[i][j] = log2e (bias_j + c q_i.se_j), then the long-range K rows, then the wave's Q rows
   // (read by every wave for dse).
   __shared__ __align__(16) bf16_t sKs[4][HAS_SE ? KSB : 16 * RV];
-  __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];     // scale_embed rows, bf16
+  // scale_embed rows as two bf16 planes, hi = bf16(se) and lo = bf16(se - hi): q.se and
+  // SE^T dS then carry se to about 2^-17 relative, as the fp32 se of the reference.
+  __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
+  __shared__ __align__(16) bf16_t sSElo[HAS_SE ? SEJ * RV : 8];
   // dS[query][tap] per wave; with scale_embed it lives in the V window once the band is done
   // (D >= 64), which leaves room for three workgroups per CU.
   constexpr bool TBL_IN_V = HAS_SE && WIN * RV * 2 >= 4 * 16 * TS * 4;
@@ -110,8 +117,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
   if constexpr (HAS_SE) {
     for (int e = tid; e < SEJ * D; e += kBlock) {
       const int j = e / D, d = e - j * D;
-      const __bf16 x = (__bf16)(j < J && p.scale_embed ? p.scale_embed[j * D + d] : 0.f);
-      sSE[j * RV + d] = __builtin_bit_cast(bf16_t, x);
+      split_bf16(j < J && p.scale_embed ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d],
+                 sSElo[j * RV + d]);
     }
   }
 
@@ -214,9 +221,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
       for (int jb = 0; jb < 3; ++jb) {
         f32x4_t acc = zero4();
         const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+        const bf16_t* srl = sSElo + (16 * jb + i) * RV + 8 * g;
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
+        for (int s = 0; s < KS; ++s) {
           acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
+          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(srl + 32 * s)), qB[s], acc);
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int j = 16 * jb + 4 * g + r;
@@ -264,14 +274,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
         ga[r] = sGain[j] * al[4 * kk + r];
         gau[r] = ga[r] * (uu[4 * kk + r] - D0);
       }
-      const s16x4_t b1 = pack_bf16x4(gau[0], gau[1], gau[2], gau[3]);
-      const s16x4_t b2 = pack_bf16x4(ga[0], ga[1], ga[2], ga[3]);
+      // The weights as bf16 hi + lo pairs: the products keep the weights' fp32 precision.
+      s16x4_t b1, b1l, b2, b2l;
+      split_bf16x4(gau[0], gau[1], gau[2], gau[3], b1, b1l);
+      split_bf16x4(ga[0], ga[1], ga[2], ga[3], b2, b2l);
       const bf16_t* kr = sK + (16 * w + 16 * kk + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const s16x4_t at = lds_read_tr16(kr + 16 * db);
         X[db] = mfma_16x16x16(at, b1, X[db]);
+        X[db] = mfma_16x16x16(at, b1l, X[db]);
         Y[db] = mfma_16x16x16(at, b2, Y[db]);
+        Y[db] = mfma_16x16x16(at, b2l, Y[db]);
       }
     }
 
@@ -281,8 +295,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
     }
     // ---- Long-range taps (diagonal of one 16x16 tile each). ----
     const bool diag = g == (i >> 2);
-    float als[NSM], uus[NSM];
     const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+    float als[NSM], uus[NSM];
 #pragma unroll
     for (int t = 0; t < NSM; ++t) {
       als[t] = 0.f; uus[t] = 0.f;
@@ -300,7 +314,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
           st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
           if constexpr (HAS_SE) {
             const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
-            const float sc = group_sum<CPR>(fmaf(c2, dot8_bf16(qR[u], se, 0.f), sGain[j] * c2 * qk));
+            const uint4 sel = *reinterpret_cast<const uint4*>(sSElo + j * RV + rc_chunk<D>(l, u) * 8);
+            const float qse = dot8_bf16(qR[u], sel, dot8_bf16(qR[u], se, 0.f));
+            const float sc = group_sum<CPR>(fmaf(c2, qse, sGain[j] * c2 * qk));
             const float raw = g_grad ? group_sum<CPR>(qk) : 0.f;
             if (rc_chunk<D>(l, u) == 0)
               *reinterpret_cast<float4*>(sPair[w][rc_row<D>(l, u)]) = float4{sc, dv, raw, 0.f};
@@ -335,13 +351,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
         if (g_grad && diag) sRAWw[i * TS + j] = c * raw;
         dlane = fmaf(alpha, uval, dlane);
         const float gal = sGain[j] * alpha;
-        const s16x4_t b1 = onehot_bf16x4(gal * (uval - D0), i & 3);
-        const s16x4_t b2 = onehot_bf16x4(gal, i & 3);
+        // One-hot weights as bf16 hi + lo pairs: the products keep the weights' fp32 precision.
+        s16x4_t b1, b1l, b2, b2l;
+        split_onehot_bf16x4(gal * (uval - D0), i & 3, b1, b1l);
+        split_onehot_bf16x4(gal, i & 3, b2, b2l);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const s16x4_t at = lds_read_tr16(ksr + 16 * db);
           X[db] = mfma_16x16x16(at, b1, X[db]);
+          X[db] = mfma_16x16x16(at, b1l, X[db]);
           Y[db] = mfma_16x16x16(at, b2, Y[db]);
+          Y[db] = mfma_16x16x16(at, b2l, Y[db]);
         }
       }
     }
@@ -387,10 +407,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
 #pragma unroll
       for (int jb = 0; jb < 3; ++jb) {
         const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
-        const s16x4_t bs = pack_bf16x4(d4.x, d4.y, d4.z, d4.w);
-        const bf16_t* sr = sSE + (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+        s16x4_t bs, bsl;
+        split_bf16x4(d4.x, d4.y, d4.z, d4.w, bs, bsl);
+        const int so = (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
-        for (int db = 0; db < DB; ++db) dQ[db] = mfma_16x16x16(lds_read_tr16(sr + 16 * db), bs, dQ[db]);
+        for (int db = 0; db < DB; ++db) {
+          const s16x4_t sh = lds_read_tr16(sSE + so + 16 * db);
+          dQ[db] = mfma_16x16x16(sh, bs, dQ[db]);
+          dQ[db] = mfma_16x16x16(sh, bsl, dQ[db]);
+          dQ[db] = mfma_16x16x16(lds_read_tr16(sSElo + so + 16 * db), bs, dQ[db]);
+        }
       }
     }
     if (row_ok) {
@@ -434,9 +460,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
 #pragma unroll
             for (int ww = 0; ww < 4; ++ww) {
               const float* col = sDS + (ww * 16 + 4 * g) * TS + 16 * jb + i;
-              const s16x4_t bs = pack_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS]);
+              s16x4_t bs, bsl;
+              split_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS], bs, bsl);
               const bf16_t* qr = sKs[ww] + (4 * g + (i >> 2)) * RV + 4 * (i & 3) + 16 * db;
-              accSE[k] = mfma_16x16x16(lds_read_tr16(qr), bs, accSE[k]);
+              const s16x4_t qt = lds_read_tr16(qr);
+              accSE[k] = mfma_16x16x16(qt, bs, accSE[k]);
+              accSE[k] = mfma_16x16x16(qt, bsl, accSE[k]);
             }
           }
         }

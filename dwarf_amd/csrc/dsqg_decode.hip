@@ -96,7 +96,8 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   const float c = p.scale;
   const long long pos = p.pos[b];
   T* outrow = static_cast<T*>(p.out) + bh * D;
-  if (pos < 0) {  // invalid position: NaN output, ring untouched
+  if (pos < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
+    if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
     if (lane < G) {
       float o[8];
 #pragma unroll

@@ -170,9 +170,11 @@ static hipError_t launch_fwd_dtype(const FwdParams& p, int D, hipStream_t st) {
 }
 
 hipError_t launch_fwd(const FwdParams& p, int dtype, int D, hipStream_t st) {
+  // fp32 runs these VALU kernels; bf16 runs only the MFMA kernel (the ABI rejects a bf16 call
+  // it cannot take with DSQG_EUNSUPPORTED before getting here).
   if (dtype == 0) return launch_fwd_dtype<float>(p, D, st);
   if (fwd_mfma_supported(p, D)) return launch_fwd_mfma(p, D, st);
-  return launch_fwd_dtype<bf16_t>(p, D, st);
+  return hipErrorNotSupported;
 }
 
 }  // namespace dsqg

@@ -13,10 +13,11 @@
 //     go through a per-wave LDS table to the lane that owns query i's taps.  An MFMA diagonal
 //     would need the operand order (16 rows x 16 bytes per 16 lanes), which the vector L1
 //     serves at about a quarter of the whole-row rate.
-//  4. Optional q.se_j term: for the dense taps SE Q^T with the same MFMA, kept per wave in an
-//     LDS table T[i][j] = bias[j] + c q_i . se_j (in the wave's staging block, which is free
-//     until the output leaves); for the long-range taps a VALU dot product folded into the
-//     score of step 3.  Without scale_embed T is the bias row.
+//  4. Optional q.se_j term: SE Q^T with the same MFMA for every tap, kept per wave in an LDS
+//     table T[i][j] = bias[j] + c q_i . se_j (in the wave's staging block, free until the
+//     long-range P V).  se is staged as bf16 hi and lo planes in the window tiles before the
+//     window rows arrive, so the term keeps se's fp32 precision.  Without scale_embed T is the
+//     bias row.
 //  5. Softmax over each query's J taps in registers: the four lanes of a query column combine
 //     max and sum with two cross-lane steps; lse = max + log(sum); the weights are normalised
 //     (and scaled by the IF gain) before P V.
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #else
   constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
 #endif
-  constexpr int TS = 38;                  // row stride of the per-wave T table (dense taps; 2-way reads)
+  constexpr int TS = 50;                  // row stride of the per-wave T table (every tap j < 48)
   constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
   constexpr int TR = NSM + (NSM & 1);     // row stride of the long-range score table (distinct banks)
   constexpr float kLog2e = 1.4426950408889634f;
@@ -60,7 +61,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   // Wave-private staging block (16 rows x RV): the T table (scale_embed), then each long-range
   // tap's V rows, then the output rows.
   __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : 16 * RV];
-  __shared__ __align__(16) bf16_t sSE[HAS_SE ? 48 * (D + 8) : 8];
   __shared__ __align__(16) float sRaw[4][16 * TR];   // per wave: long-range q.k [query][tap]
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
@@ -126,12 +126,36 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
     sGain2[j] = (p.score_gain ? p.score_gain[h * J + j] : 1.0f) * c2;
   }
+  float* sTw = reinterpret_cast<float*>(sVs[w]);  // T table until the long-range P V
   if constexpr (HAS_SE) {
+    // T[i][j] = log2e (bias_j + c q_i.se_j) for every tap, SE Q^T on the MFMA.  scale_embed is
+    // staged as two bf16 planes, hi = bf16(se) in the K window and lo = bf16(se - hi) in the V
+    // window (both still free: the window rows are in flight in registers), so q.se keeps se's
+    // fp32 precision to about 2^-17.
+    bf16_t* const sSE = sK;
+    bf16_t* const sSElo = sV;
     for (int e = tid; e < 48 * D; e += kBlock) {
       const int j = e / D, d = e - j * D;
-      const __bf16 x = (__bf16)(j < J ? p.scale_embed[j * D + d] : 0.f);
-      sSE[j * (D + 8) + d] = __builtin_bit_cast(bf16_t, x);
+      split_bf16(j < J ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d], sSElo[j * RV + d]);
     }
+    __syncthreads();
+#pragma unroll
+    for (int jb = 0; jb < 3; ++jb) {
+      f32x4_t acc = zero4();
+      const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+      const bf16_t* srl = sSElo + (16 * jb + i) * RV + 8 * g;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
+        acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(srl + 32 * s)), qB[s], acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jb + 4 * g + r;
+        if (j < J) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+      }
+    }
+    __syncthreads();  // every wave has read the planes: the window rows move in
   }
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
@@ -159,17 +183,13 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   // (DPP), and one lane per row files the score in the wave's [query][tap] table.  The first
   // half's registers are free before the second half is loaded.
   float* sRw = sRaw[w];
-  // Score of long-range tap t for each of the wave's rows, less the bias (log2 units):
-  // gain c log2e q.k (+ c log2e q.se_j), one DPP sum per row.
+  // Score of long-range tap t for each of the wave's rows, less the bias and q.se term
+  // (log2 units): gain c log2e q.k, one DPP sum per row.
   auto sparse_score = [&](int t) {
     const int j = W + 1 + t;
 #pragma unroll
     for (int u = 0; u < CHW; ++u) {
       float d = sGain2[j] * dot8_bf16(qR[u], kS[t][u], 0.f);
-      if constexpr (HAS_SE) {
-        const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * (D + 8) + rc_chunk<D>(l, u) * 8);
-        d = fmaf(c2, dot8_bf16(qR[u], se, 0.f), d);
-      }
       d = group_sum<CPR>(d);
       if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * TR + t] = d;
     }
@@ -200,25 +220,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 
   __builtin_amdgcn_sched_barrier(0);
 
-  float* sTw = reinterpret_cast<float*>(sVs[w]);  // T table until the output exchange
-  if constexpr (HAS_SE) {
-#pragma unroll
-    for (int jb = 0; jb < 3; ++jb) {
-      f32x4_t acc = zero4();
-      const bf16_t* sr = sSE + (16 * jb + i) * (D + 8) + 8 * g;
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * jb + 4 * g + r;
-        if (j <= W) sTw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's table is written
-    __builtin_amdgcn_wave_barrier();
-  }
-
   // Scores in log2 units: s2 = gain*c*log2e * q.k + log2e*(bias + c q.se).
   float sd[12];
   const int dl0 = 32 - 4 * g + i;
@@ -248,7 +249,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     ss[t] = -INFINITY;
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      const float v = sRw[i * TR + t] + sBias2[j];
+      const float v = sRw[i * TR + t] + (HAS_SE ? sTw[i * TS + j] : sBias2[j]);
       ss[t] = (diag && row_ok && n >= dl_s[t]) ? v : -INFINITY;
     }
   }

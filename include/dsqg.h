@@ -55,7 +55,10 @@ typedef struct ihipStream_t* dsqg_stream_t;
 typedef enum {
     DSQG_OK = 0,
     DSQG_EINVAL = 1,        /* bad shape, stride, alignment, pointer or offset table */
-    DSQG_EUNSUPPORTED = 2,  /* valid arguments this build has no kernel for (e.g. D) */
+    DSQG_EUNSUPPORTED = 2,  /* valid arguments this build has no kernel for: the head dim,
+                               J > 48, or (bf16) more than 16 offsets beyond the dense
+                               window delta = 0, 1, 2, ... or a slice whose rows a 32-bit
+                               byte offset cannot reach */
     DSQG_EHIP = 3,          /* a HIP launch failed (hipGetLastError after the launch) */
     DSQG_EWORKSPACE = 4     /* workspace pointer NULL or smaller than required */
 } dsqg_status;
@@ -121,7 +124,9 @@ typedef struct {
  * int64) is the absolute position of the new token.  The step writes k_new / v_new into slot
  * pos mod S, then attends slot (pos - delta_j) mod S for delta_j > 0 and the new row for
  * delta_j == 0; taps with pos - delta_j < 0 are masked (never wrapped).  If pos_next is non-NULL
- * (and distinct from pos) it receives pos + 1, so a captured step can be replayed. */
+ * (and distinct from pos) it receives pos + 1, so a captured step can be replayed.  A negative
+ * pos marks an invalid sequence: its output is NaN, its rings are untouched, and pos_next
+ * receives the same negative value, so it stays invalid over replays. */
 typedef struct {
     dsqg_shape shape;
     int32_t S;                 /* ring slots */

@@ -18,3 +18,15 @@ def gpu_device():
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU visible")
     return torch.device("cuda:0")
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """Per-tensor parity errors of the GPU tests (max error / worst ratio to the bound)."""
+    try:
+        from tests.tolerance import SUMMARY
+    except ImportError:
+        from tolerance import SUMMARY  # tests/ on sys.path
+    if SUMMARY:
+        terminalreporter.write_sep("-", "parity: max abs error / worst ratio to the bound")
+        for line in SUMMARY:
+            terminalreporter.write_line(line)

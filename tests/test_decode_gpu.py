@@ -1,8 +1,9 @@
 """GPU parity of the ring-buffer decode step (workload 4) against the CPU oracle.
 
-Tolerance: bf16 outputs vs the fp32 oracle on the same bf16 inputs, max|x - ref| <= 2e-2 *
-max(1, max|ref|); fp32 outputs vs the float64 oracle, <= 1e-5 * max|ref|.  Ring contents are
-compared bit for bit (the step copies rows).
+Tolerance (tests/tolerance.py): bf16 outputs vs the fp32 oracle on the same bf16 inputs,
+elementwise |x - ref| <= 2e-2 + 2^-9 |ref| (the output is stored in bf16); fp32 outputs vs the
+float64 oracle, max|x - ref| <= 1e-5 * max|ref|.  Ring contents are compared bit for bit (the
+step copies rows).
 """
 
 import pytest
@@ -13,6 +14,7 @@ from dwarf_amd import ops
 from dwarf_amd.offsets import OFFSETS_J46, OFFSETS_J47, OFFSETS_V3
 from dwarf_amd.workloads import DECODE, make_decode_inputs
 from oracle import decode_step, dsqg_forward
+from tests import tolerance
 
 pytestmark = pytest.mark.gpu
 
@@ -23,6 +25,11 @@ def _say(msg):
 
 def _err(got, ref):
     return (got.double() - ref.double()).abs().max().item(), ref.abs().max().item()
+
+
+def _bf16_ratio(got, ref):
+    """Worst ratio of the elementwise error to the bf16-stored bound (<= 1 passes)."""
+    return tolerance.elementwise_ratio("decode", got, ref)[1]
 
 
 def test_decode_workload_1000_steps(gpu_device):
@@ -45,12 +52,14 @@ def test_decode_workload_1000_steps(gpu_device):
         ref = decode_step(q.float(), kn.float(), vn.float(), k_ring_ref, v_ring_ref, pos,
                           inp["pos_bias"])
         err, scale = _err(out, ref)
+        ratio = _bf16_ratio(out, ref)
         worst = max(worst, err)
-        assert err <= 2e-2 * max(1.0, scale), f"step {step}: err {err:.3e}"
+        assert ratio <= 1.0, f"step {step}: err {err:.3e} (ratio {ratio:.2f})"
         pos = pos + 1
         if step % 200 == 0:
             _say(f"step {step} err {err:.3e}")
     _say(f"{steps} steps, worst err {worst:.3e}")
+    tolerance.SUMMARY.append(f"decode workload 4, {steps} steps: worst max err {worst:.2e}")
     assert torch.equal(d["k_ring"].cpu(), k_ring_ref)
     assert torch.equal(d["v_ring"].cpu(), v_ring_ref)
 
@@ -84,10 +93,14 @@ def test_decode_equals_full_sequence_row(gpu_device, dtype, p, D):
     ref = dsqg_forward(qs.to(cd), ks.to(cd), vs.to(cd), pb.to(cd), se.to(cd), OFFSETS_V3,
                        sg.to(cd), a.to(cd))[:, :, p]
     err, scale = _err(out, ref)
-    bound = 1e-5 * scale if dtype == torch.float32 else 2e-2 * max(1.0, scale)
-    _say(f"p={p} D={D} {dtype}: err {err:.3e} bound {bound:.3e}")
     assert torch.isfinite(out).all()
-    assert err <= bound
+    if dtype == torch.float32:
+        _say(f"p={p} D={D} {dtype}: err {err:.3e} bound {1e-5 * scale:.3e}")
+        assert err <= 1e-5 * scale
+    else:
+        ratio = _bf16_ratio(out, ref)
+        _say(f"p={p} D={D} {dtype}: err {err:.3e} ratio {ratio:.2f}")
+        assert ratio <= 1.0
     assert int(cache.pos[0]) == p + 1
 
 
@@ -117,8 +130,7 @@ def test_decode_pos_next_and_graph_replay(gpu_device):
     ref = decode_step(inp["q"].float(), inp["k_new"].float(), inp["v_new"].float(), k_ref, v_ref,
                       pos, inp["pos_bias"])
     assert torch.equal(pos_b.cpu(), pos + 1)
-    err, scale = _err(out.cpu(), ref)
-    assert err <= 2e-2 * max(1.0, scale)
+    assert _bf16_ratio(out.cpu(), ref) <= 1.0
 
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=s):
@@ -134,7 +146,7 @@ def test_decode_pos_next_and_graph_replay(gpu_device):
         # the graph's second step is the last one; out holds its result
         err, scale = _err(out.cpu(), ref)
         _say(f"replay {rep}: err {err:.3e}")
-        assert err <= 2e-2 * max(1.0, scale)
+        assert _bf16_ratio(out.cpu(), ref) <= 1.0
         assert torch.equal(pos_b.cpu(), pos + 1)
     assert torch.equal(d["k_ring"].cpu(), k_ref) and torch.equal(d["v_ring"].cpu(), v_ref)
 
@@ -159,7 +171,49 @@ def test_decode_other_offset_tables(gpu_device, offsets, p, dtype):
     cd = torch.float64 if dtype == torch.float32 else torch.float32
     ref = dsqg_forward(qs.to(cd), ks.to(cd), vs.to(cd), pb.to(cd), None, list(offsets))[:, :, p]
     err, scale = _err(out, ref)
-    bound = 1e-5 * scale if dtype == torch.float32 else 2e-2 * max(1.0, scale)
-    _say(f"J={J} p={p} {dtype}: err {err:.3e} bound {bound:.3e}")
+    _say(f"J={J} p={p} {dtype}: err {err:.3e}")
     assert torch.isfinite(out).all()
-    assert err <= bound
+    if dtype == torch.float32:
+        assert err <= 1e-5 * scale
+    else:
+        assert _bf16_ratio(out, ref) <= 1.0
+
+
+def test_decode_negative_position_stays_invalid_over_replays(gpu_device):
+    """A negative position gives a NaN output row, leaves that sequence's rings untouched, and
+    writes the same negative value to pos_next, so a pos / pos_next ping-pong replay keeps the
+    sequence invalid; the other sequences step normally."""
+    B, H, D, S = 3, 2, 64, 1537
+    inp = make_decode_inputs(B=B, H=H, D=D, S=S, seed=11)
+    d = {k: v.to(gpu_device) for k, v in inp.items()}
+    k_ref, v_ref = inp["k_ring"].clone(), inp["v_ring"].clone()
+    pos0 = inp["pos"].clone()
+    pos0[1] = -5
+    pos_a = pos0.to(gpu_device)
+    pos_b = torch.full_like(pos_a, 12345)
+    out = torch.empty_like(d["q"])
+    offs = list(OFFSETS_V3)
+
+    def step(src, dst):
+        ops.decode_step_into(d["q"], d["k_new"], d["v_new"], d["k_ring"], d["v_ring"], src,
+                             d["pos_bias"], None, None, None, offs, out, dst)
+
+    pos = pos0.clone()
+    for rep in range(4):
+        src, dst = (pos_a, pos_b) if rep % 2 == 0 else (pos_b, pos_a)
+        step(src, dst)
+        torch.cuda.synchronize(gpu_device)
+        valid = torch.tensor([0, 2])
+        kv, vv = k_ref[valid].clone(), v_ref[valid].clone()   # the oracle writes its rings
+        ref = decode_step(inp["q"][valid].float(), inp["k_new"][valid].float(),
+                          inp["v_new"][valid].float(), kv, vv, pos[valid], inp["pos_bias"])
+        k_ref[valid], v_ref[valid] = kv, vv
+        o = out.cpu()
+        assert torch.isnan(o[1]).all()
+        assert _bf16_ratio(o[valid], ref) <= 1.0
+        nxt = dst.cpu()
+        assert int(nxt[1]) == -5, f"replay {rep}: pos_next of the invalid sequence {int(nxt[1])}"
+        assert torch.equal(nxt[valid], pos[valid] + 1)
+        pos[valid] += 1
+    assert torch.equal(d["k_ring"][1].cpu(), inp["k_ring"][1])
+    assert torch.equal(d["v_ring"][1].cpu(), inp["v_ring"][1])
