@@ -19,6 +19,8 @@ MAX_OFFSETS = 64
 ABI_VERSION = 1
 
 DSQG_OK, DSQG_EINVAL, DSQG_EUNSUPPORTED, DSQG_EHIP, DSQG_EWORKSPACE = 0, 1, 2, 3, 4
+DSQG_ETOOLARGE = 5
+NOALLOC_SCRATCH_BYTES = 64 << 20  # DSQG_NOALLOC_SCRATCH_BYTES
 DSQG_F32, DSQG_BF16, DSQG_F16 = 0, 1, 2
 
 _i64x4 = ctypes.c_int64 * 4
@@ -102,6 +104,7 @@ SIGNATURES = {
     "dsqg_bwd_dq": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
     "dsqg_bwd_dkdv": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
     "dsqg_bwd_params": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
+    "dsqg_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
     "dsqg_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), _vp]),
     "dsqg_pool_gate_workspace_size": (ctypes.c_int, [ctypes.c_int32, ctypes.c_int32,
                                                      ctypes.c_int32, ctypes.c_int,

@@ -6,6 +6,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/dsqg.h"
 #include "dsqg_common.hpp"
 #include "dsqg_launch.hpp"
@@ -123,6 +125,9 @@ const char* dsqg_status_string(int status) {
              "more than 16 offsets beyond the dense window)";
     case DSQG_EHIP: return "HIP launch error";
     case DSQG_EWORKSPACE: return "workspace missing or too small";
+    case DSQG_ETOOLARGE:
+      return "the call needs more workspace than dsqg_bwd_noalloc's static scratch "
+             "(DSQG_NOALLOC_SCRATCH_BYTES); use dsqg_bwd with a workspace";
     default: return "unknown status";
   }
 }
@@ -176,17 +181,28 @@ int dsqg_bwd_workspace_size(const dsqg_bwd_args* a, size_t* bytes) {
 // Phase selector for the backward entry points.
 enum { kPhaseDq = 1, kPhaseDkdv = 2, kPhaseParams = 4, kPhaseAll = 7 };
 
-static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
+// Workspace source of a backward call: the caller's (args->workspace), or the static scratch
+// of dsqg_bwd_noalloc.
+static int scratch_for_stream(hipStream_t st, void** ptr);
+
+static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream, bool use_scratch) {
   BwdParams p;
   int st = check_bwd(a, &p);
   if (st) return st;
   const dsqg_shape& s = a->shape;
   const BwdLayout L = bwd_layout(*a, p);
-  if (L.total > 0) {
+  char* ws = static_cast<char*>(a->workspace);
+  if (use_scratch) {
+    // Sizes are checked before any HIP call; the scratch pointer of this stream's device is
+    // taken (once per device) only for a call that fits.
+    if (L.total > DSQG_NOALLOC_SCRATCH_BYTES) return DSQG_ETOOLARGE;
+    void* sp = nullptr;
+    if (L.total > 0 && (st = scratch_for_stream(reinterpret_cast<hipStream_t>(stream), &sp))) return st;
+    ws = static_cast<char*>(sp);
+  } else if (L.total > 0) {
     if (!a->workspace || a->workspace_bytes < L.total) return DSQG_EWORKSPACE;
     if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0) return DSQG_EINVAL;
   }
-  char* ws = static_cast<char*>(a->workspace);
   p.scale = 1.0f / sqrtf((float)s.D);
   p.q = a->q; p.qs = to_strides(a->q_stride);
   p.k = a->k; p.ks = to_strides(a->k_stride);
@@ -238,13 +254,20 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream) {
   return DSQG_OK;
 }
 
-int dsqg_bwd(const dsqg_bwd_args* a, dsqg_stream_t stream) { return run_bwd(a, kPhaseAll, stream); }
-int dsqg_bwd_dq(const dsqg_bwd_args* a, dsqg_stream_t stream) { return run_bwd(a, kPhaseDq, stream); }
+int dsqg_bwd(const dsqg_bwd_args* a, dsqg_stream_t stream) {
+  return run_bwd(a, kPhaseAll, stream, false);
+}
+int dsqg_bwd_dq(const dsqg_bwd_args* a, dsqg_stream_t stream) {
+  return run_bwd(a, kPhaseDq, stream, false);
+}
 int dsqg_bwd_dkdv(const dsqg_bwd_args* a, dsqg_stream_t stream) {
-  return run_bwd(a, kPhaseDkdv, stream);
+  return run_bwd(a, kPhaseDkdv, stream, false);
 }
 int dsqg_bwd_params(const dsqg_bwd_args* a, dsqg_stream_t stream) {
-  return run_bwd(a, kPhaseParams, stream);
+  return run_bwd(a, kPhaseParams, stream, false);
+}
+int dsqg_bwd_noalloc(const dsqg_bwd_args* a, dsqg_stream_t stream) {
+  return run_bwd(a, kPhaseAll, stream, true);
 }
 
 int dsqg_decode_step(const dsqg_decode_args* a, dsqg_stream_t stream) {
@@ -282,3 +305,44 @@ int dsqg_decode_step(const dsqg_decode_args* a, dsqg_stream_t stream) {
 namespace dsqg {
 bool head_dim_supported(int D) { return D == 32 || D == 64 || D == 128; }
 }  // namespace dsqg
+
+// ---------------------------------------------------------------------------------------------
+// Static scratch of dsqg_bwd_noalloc: the backward's workspace (D', parameter-gradient partials)
+// in a file-scope device array, so that the call allocates nothing.  Each device the library
+// runs on holds its own copy for the life of the process.  Host code never uses the array's
+// name as an address (on the host it is only a stand-in): the device address comes from
+// hipGetSymbolAddress, taken once per device with that device current, and is kept per device.
+// Every word the kernels read is written earlier in the same call, so nothing needs clearing
+// between calls; calls that overlap on one device share the array and race.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[DSQG_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static int scratch_for_stream(hipStream_t st, void** ptr) {
+  int dev = -1;
+  if (st) {
+    if (hipStreamGetDevice(st, &dev) != hipSuccess) return DSQG_EHIP;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return DSQG_EHIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return DSQG_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return DSQG_EHIP;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return DSQG_EHIP;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return DSQG_EHIP;
+    if (e != hipSuccess || !p) return DSQG_EHIP;
+    if ((reinterpret_cast<uintptr_t>(p) & 255u) != 0) return DSQG_EHIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return DSQG_OK;
+}

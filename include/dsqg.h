@@ -60,8 +60,14 @@ typedef enum {
                                window delta = 0, 1, 2, ... or a slice whose rows a 32-bit
                                byte offset cannot reach */
     DSQG_EHIP = 3,          /* a HIP launch failed (hipGetLastError after the launch) */
-    DSQG_EWORKSPACE = 4     /* workspace pointer NULL or smaller than required */
+    DSQG_EWORKSPACE = 4,    /* workspace pointer NULL or smaller than required */
+    DSQG_ETOOLARGE = 5      /* dsqg_bwd_noalloc: the call needs more than its static scratch */
 } dsqg_status;
+
+/* Static scratch of dsqg_bwd_noalloc (bytes per device): the backward workspace of the largest
+ * call it takes, as dsqg_bwd_workspace_size reports it (e.g. 37 MB for B8 H12 N2048 D64 with
+ * dscale_embed, 1.3 MB without). */
+#define DSQG_NOALLOC_SCRATCH_BYTES (64u << 20)
 
 /* DSQG_F16 is accepted by the pool entry points only. */
 typedef enum { DSQG_F32 = 0, DSQG_BF16 = 1, DSQG_F16 = 2 } dsqg_dtype;
@@ -169,6 +175,16 @@ int dsqg_bwd(const dsqg_bwd_args* args, dsqg_stream_t stream);
 int dsqg_bwd_dq(const dsqg_bwd_args* args, dsqg_stream_t stream);
 int dsqg_bwd_dkdv(const dsqg_bwd_args* args, dsqg_stream_t stream);
 int dsqg_bwd_params(const dsqg_bwd_args* args, dsqg_stream_t stream);
+
+/* dsqg_bwd without a workspace argument and without any allocation: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  args->workspace and workspace_bytes
+ * are ignored; the workspace is a static scratch array of DSQG_NOALLOC_SCRATCH_BYTES on each
+ * device, whose address is looked up once per device on the first call there.  A call whose
+ * workspace (dsqg_bwd_workspace_size) exceeds it returns DSQG_ETOOLARGE before any HIP call.
+ * Same kernels, outputs and stream rules as dsqg_bwd; calls that overlap on one device (other
+ * streams, other threads) share the scratch and race, so serialise them. */
+int dsqg_bwd_noalloc(const dsqg_bwd_args* args, dsqg_stream_t stream);
 
 int dsqg_decode_step(const dsqg_decode_args* args, dsqg_stream_t stream);
 
