@@ -133,7 +133,7 @@ const char* dsqg_status_string(int status) {
 }
 
 int dsqg_supported_head_dims(int32_t* dims, int cap) {
-  static const int32_t kDims[] = {32, 64, 128};
+  static const int32_t kDims[] = {32, 64, 80, 96, 128};
   const int n = (int)(sizeof(kDims) / sizeof(kDims[0]));
   for (int i = 0; i < n && i < cap; ++i) dims[i] = kDims[i];
   return n;
@@ -303,7 +303,7 @@ int dsqg_decode_step(const dsqg_decode_args* a, dsqg_stream_t stream) {
 }  // extern "C"
 
 namespace dsqg {
-bool head_dim_supported(int D) { return D == 32 || D == 64 || D == 128; }
+bool head_dim_supported(int D) { return D == 32 || D == 64 || D == 80 || D == 96 || D == 128; }
 }  // namespace dsqg
 
 // ---------------------------------------------------------------------------------------------

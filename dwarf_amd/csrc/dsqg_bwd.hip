@@ -38,14 +38,14 @@ bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
   const long long all[4] = {p.qs.n, p.ks.n, p.vs.n, p.dos.n};
   for (long long x : all) { rs = x > rs ? x : rs; rmin = x < rmin ? x : rmin; }
   const long long span = ((long long)p.N + p.taps.maxd + 64) * rs * 2;
-  return (D == 32 || D == 64 || D == 128) && p.taps.J - p.taps.W - 1 <= kMaxSparse &&
+  return (D == 32 || D == 64 || D == 80 || D == 96 || D == 128) && p.taps.J - p.taps.W - 1 <= kMaxSparse &&
          rmin >= D && span < (1LL << 31);
 }
 
 void bwd_plan(BwdParams& p, int D, int dtype) {
   const bool mfma = bwd_mfma_supported(p, D, dtype);
-  const int QPB = mfma ? 64 : kBlock / (D / 8);  // dq rows per tile
-  const int KPB = mfma ? 64 : kBlock / (D / 8);  // dk/dv rows per workgroup
+  const int QPB = mfma ? 64 : kBlock / lanes_per_row(D);  // dq rows per tile
+  const int KPB = mfma ? 64 : kBlock / lanes_per_row(D);  // dk/dv rows per workgroup
   p.n_tiles = (p.N + QPB - 1) / QPB;
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
   // One tile per workgroup: the partial rows (J floats, and J x D for dscale_embed) are small next

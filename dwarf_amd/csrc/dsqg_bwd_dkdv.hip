@@ -14,7 +14,7 @@ namespace dsqg {
 
 template <typename T, int D, int JMAX, bool HAS_SE>
 __global__ __launch_bounds__(kBlock) void bwd_dkdv_kernel(BwdParams p) {
-  constexpr int G = D / 8;
+  constexpr int G = lanes_per_row(D);  // lanes with 8g >= D (D = 80, 96) hold zeros
   constexpr int QPB = kBlock / G;
   constexpr int ROWS = QPB + kMaxWindow;
   constexpr int CPR = D * (int)sizeof(T) / 16;
@@ -70,9 +70,10 @@ __global__ __launch_bounds__(kBlock) void bwd_dkdv_kernel(BwdParams p) {
   const int m = m0 + ki;
   const bool key_ok = m < N;
   const int d0 = g * 8;
+  const bool lane_ok = d0 < D;
 
   float kx[8], vx[8];
-  if (key_ok) {
+  if (key_ok && lane_ok) {
     Vec8<T>::load(kb + m * p.ks.n + d0, kx);
     Vec8<T>::load(vb + m * p.vs.n + d0, vx);
   } else {
@@ -89,16 +90,22 @@ __global__ __launch_bounds__(kBlock) void bwd_dkdv_kernel(BwdParams p) {
       const int n = m + p.taps.delta[j];
       const bool ok = key_ok && n < N;
       float qx[8], dx[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { qx[e] = 0.f; dx[e] = 0.f; }
       float ps = 0.f, pu = 0.f, lse = 0.f, Dp = 0.f;
       if (ok) {
         if (j <= W) {
-          Vec8<T>::load(sQ + (n - m0) * D + d0, qx);
-          Vec8<T>::load(sDO + (n - m0) * D + d0, dx);
+          if (lane_ok) {
+            Vec8<T>::load(sQ + (n - m0) * D + d0, qx);
+            Vec8<T>::load(sDO + (n - m0) * D + d0, dx);
+          }
           lse = sL[n - m0];
           Dp = sDp[n - m0];
         } else {
-          Vec8<T>::load(qb + n * p.qs.n + d0, qx);
-          Vec8<T>::load(dob + n * p.dos.n + d0, dx);
+          if (lane_ok) {
+            Vec8<T>::load(qb + n * p.qs.n + d0, qx);
+            Vec8<T>::load(dob + n * p.dos.n + d0, dx);
+          }
           lse = p.lse[rowbase + n];
           Dp = p.dpre[rowbase + n];
         }
@@ -107,8 +114,10 @@ __global__ __launch_bounds__(kBlock) void bwd_dkdv_kernel(BwdParams p) {
         for (int e = 0; e < 8; ++e) { pk = fmaf(qx[e], kx[e], pk); pu = fmaf(dx[e], vx[e], pu); }
         ps = pk * sGain[j];
         if constexpr (HAS_SE) {
+          if (lane_ok) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) ps = fmaf(qx[e], sSE[j * D + d0 + e], ps);
+            for (int e = 0; e < 8; ++e) ps = fmaf(qx[e], sSE[j * D + d0 + e], ps);
+          }
         }
       }
       const float ts = group_sum<G>(ps);
@@ -122,7 +131,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dkdv_kernel(BwdParams p) {
       }
     }
   }
-  if (key_ok) {
+  if (key_ok && lane_ok) {
     Vec8<T>::store(static_cast<T*>(p.dk) + b * p.dks.b + h * p.dks.h + m * p.dks.n + d0, dk);
     Vec8<T>::store(static_cast<T*>(p.dv) + b * p.dvs.b + h * p.dvs.h + m * p.dvs.n + d0, dv);
   }
@@ -143,6 +152,8 @@ static hipError_t launch_bwd_dkdv_dtype(const BwdParams& p, int D, unsigned nb, 
   switch (D) {
     case 32: return launch_bwd_dkdv_d<T, 32>(p, nb, st);
     case 64: return launch_bwd_dkdv_d<T, 64>(p, nb, st);
+    case 80: return launch_bwd_dkdv_d<T, 80>(p, nb, st);
+    case 96: return launch_bwd_dkdv_d<T, 96>(p, nb, st);
     case 128: return launch_bwd_dkdv_d<T, 128>(p, nb, st);
     default: return hipErrorInvalidValue;
   }

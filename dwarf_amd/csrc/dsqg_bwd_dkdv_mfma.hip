@@ -34,15 +34,18 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_dkdv_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 4))) void bwd_dkdv_mfma_kernel(BwdParams p) {
+  using G_ = Geo<D>;
   constexpr int KT = 64;                  // key rows per workgroup
-  constexpr int KS = D / 32;
-  constexpr int DB = D / 16;
-  constexpr int RV = D + 8;               // LDS row stride (36 dwords at D=64)
+  constexpr int KS = G_::KS;
+  constexpr int DB = G_::DB;
+  constexpr int RV = G_::RV;              // LDS row stride (36 dwords at D=64)
   constexpr int WIN = KT + kMaxWindow;    // query window rows [m0, m0+96)
-  constexpr int CPR = D / 8;
-  constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
-  constexpr int CHW = D / 32;             // 16-byte chunks per lane of a wave's 16-row block
+  constexpr int CPR = G_::CPR;
+  constexpr int CPS = G_::CPS;            // chunks per staged (padded) row
+  constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
+  constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
+  constexpr int CPRP = G_::CPRP;          // lanes per row in the row-chunk layout
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;
   // [query][dense tap] table row stride: a 36-word pitch spreads the band's diagonal reads
@@ -96,10 +99,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
   int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
-    qlaneR[u] = opaque(rc_row<D>(l, u) * qsn + rc_chunk<D>(l, u) * 8);
-    olaneR[u] = opaque(rc_row<D>(l, u) * dosn + rc_chunk<D>(l, u) * 8);
-    klaneR[u] = opaque(rc_row<D>(l, u) * ksn + rc_chunk<D>(l, u) * 8);
-    vlaneR[u] = opaque(rc_row<D>(l, u) * vsn + rc_chunk<D>(l, u) * 8);
+    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
+    olaneR[u] = opaque(rc_lane<D>(l, u, dosn));
+    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
+    vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
   }
 
   // ---- Loads. ----
@@ -107,14 +110,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
-    wq[u] = bload16(rQ, m0 * qsn + opaque((ci / CPR) * qsn + (ci % CPR) * 8));
-    wo[u] = bload16(rO, m0 * dosn + opaque((ci / CPR) * dosn + (ci % CPR) * 8));
+    const bool cv = ci % CPS < CPR;
+    wq[u] = bload16(rQ, m0 * qsn + opaque(cv ? (ci / CPS) * qsn + (ci % CPS) * 8 : kNoElem));
+    wo[u] = bload16(rO, m0 * dosn + opaque(cv ? (ci / CPS) * dosn + (ci % CPS) * 8 : kNoElem));
   }
   bf16x8_t kB[KS], vB[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    kB[s] = as_bf16x8(bload16(rK, m0w * ksn + klane + 32 * s));
-    vB[s] = as_bf16x8(bload16(rV, m0w * vsn + vlane + 32 * s));
+    const bool sv = 8 * g + 32 * s < D;  // the zero columns of D = 80's last K-step
+    kB[s] = as_bf16x8(bload16(rK, m0w * ksn + (sv ? klane + 32 * s : kNoElem)));
+    vB[s] = as_bf16x8(bload16(rV, m0w * vsn + (sv ? vlane + 32 * s : kNoElem)));
   }
   uint4 kR[CHW], vR[CHW];
 #pragma unroll
@@ -149,18 +154,19 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
     sGainC[j] = gj * c;
   }
   if constexpr (HAS_SE) {
-    for (int e = tid; e < SEJ * D; e += kBlock) {
-      const int j = e / D, d = e - j * D;
-      const float x = j < J ? p.scale_embed[j * D + d] : 0.f;
+    constexpr int DP = G_::DP;
+    for (int e = tid; e < SEJ * DP; e += kBlock) {
+      const int j = e / DP, d = e - j * DP;
+      const float x = j < J && d < D ? p.scale_embed[j * D + d] : 0.f;
       sSE[j * RV + d] = __builtin_bit_cast(bf16_t, (__bf16)x);
     }
   }
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
-    if (ci < WIN * CPR) {
-      st16(sQ + (ci / CPR) * RV + (ci % CPR) * 8, wq[u]);
-      st16(sO + (ci / CPR) * RV + (ci % CPR) * 8, wo[u]);
+    if (ci < WIN * CPS) {
+      st16(sQ + (ci / CPS) * RV + (ci % CPS) * 8, wq[u]);
+      st16(sO + (ci / CPS) * RV + (ci % CPS) * 8, wo[u]);
     }
   }
   __syncthreads();
@@ -277,13 +283,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE ? 3 : 4)) void bwd_d
       for (int u = 0; u < CHW; ++u) {
         float sk = sGain2[j] * dot8_bf16(qS[t % PF][u], kR[u], 0.f);
         if constexpr (HAS_SE) {
-          const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
+          // Lanes past the row read chunk 0 (finite) against their zero query chunk.
+          const int sc8 = rc_valid<D>(l, u) ? rc_chunk<D>(l, u) * 8 : 0;
+          const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + sc8);
           sk = fmaf(c2, dot8_bf16(qS[t % PF][u], se, 0.f), sk);
         }
-        const float dk = group_sum<CPR>(sk);
-        const float dv = group_sum<CPR>(dot8_bf16(oS[t % PF][u], vR[u], 0.f));
-        st16(qsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qS[t % PF][u]);
-        st16(osw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, oS[t % PF][u]);
+        const float dk = group_sum<CPRP>(sk);
+        const float dv = group_sum<CPRP>(dot8_bf16(oS[t % PF][u], vR[u], 0.f));
+        if (rc_valid<D>(l, u)) {
+          st16(qsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qS[t % PF][u]);
+          st16(osw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, oS[t % PF][u]);
+        }
         if (rc_chunk<D>(l, u) == 0) sPair[w][rc_row<D>(l, u)] = float2{dk, dv};
       }
       if (t + PF < NS) {
@@ -345,6 +355,8 @@ hipError_t launch_bwd_dkdv_mfma(const BwdParams& p, int D, unsigned nblocks, hip
   switch (D) {
     case 32: return launch_dkdv_mfma_d<32>(p, nblocks, st);
     case 64: return launch_dkdv_mfma_d<64>(p, nblocks, st);
+    case 80: return launch_dkdv_mfma_d<80>(p, nblocks, st);
+    case 96: return launch_dkdv_mfma_d<96>(p, nblocks, st);
     case 128: return launch_dkdv_mfma_d<128>(p, nblocks, st);
     default: return hipErrorInvalidValue;
   }

@@ -21,7 +21,7 @@ namespace dsqg {
 
 template <typename T, int D, int JMAX, bool HAS_SE>
 __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
-  constexpr int G = D / 8;
+  constexpr int G = lanes_per_row(D);  // lanes with 8g >= D (D = 80, 96) hold zeros
   constexpr int QPB = kBlock / G;
   constexpr int ROWS = QPB + kMaxWindow;
   constexpr int CPR = D * (int)sizeof(T) / 16;
@@ -70,6 +70,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
 
   const int qi = tid / G, g = tid - qi * G;
   const int d0 = g * 8;
+  const bool lane_ok = d0 < D;
   const int t_begin = chunk * p.tiles_per_block;
   const int t_end = min(p.n_tiles, t_begin + p.tiles_per_block);
 
@@ -91,10 +92,10 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
     const bool row_ok = n < N;
     float q[8], dO[8];
     float lse = 0.f;
-    if (row_ok) {
+    if (row_ok) lse = p.lse[rowbase + n];
+    if (row_ok && lane_ok) {
       Vec8<T>::load(qb + n * p.qs.n + d0, q);
       Vec8<T>::load(dob + n * p.dos.n + d0, dO);
-      lse = p.lse[rowbase + n];
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) { q[e] = 0.f; dO[e] = 0.f; }
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
         const int m = n - p.taps.delta[j];
         const bool ok = row_ok && m >= 0;
         float ps = 0.f, pk = 0.f, pu = 0.f;
-        if (ok) {
+        if (ok && lane_ok) {
           float kx[8], vx[8];
           if (j <= W) {
             Vec8<T>::load(sK + (m - base) * D + d0, kx);
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
       if (j < J) {
         const float dS = a * al[j] * (u[j] - Dp);
         u[j] = dS;
-        if (al[j] > 0.f) {
+        if (al[j] > 0.f && lane_ok) {
           const int m = n - p.taps.delta[j];
           float kx[8];
           if (j <= W) Vec8<T>::load(sK + (m - base) * D + d0, kx);
@@ -162,7 +163,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
     if (row_ok) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) dq[e] *= c;
-      Vec8<T>::store(dqb + n * p.dqs.n + d0, dq);
+      if (lane_ok) Vec8<T>::store(dqb + n * p.dqs.n + d0, dq);
       if (g == 0) p.dpre[rowbase + n] = Dp;
     }
 
@@ -177,7 +178,7 @@ __global__ __launch_bounds__(kBlock) void bwd_dq_kernel(BwdParams p) {
       }
       sDp[qi] = row_ok ? Dp : 0.f;
     }
-    if (se_grad) {
+    if (se_grad && lane_ok) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) sQ[qi * D + d0 + e] = q[e];
     }
@@ -239,6 +240,8 @@ static hipError_t launch_bwd_dq_dtype(const BwdParams& p, int D, unsigned nb, hi
   switch (D) {
     case 32: return launch_bwd_dq_d<T, 32>(p, nb, st);
     case 64: return launch_bwd_dq_d<T, 64>(p, nb, st);
+    case 80: return launch_bwd_dq_d<T, 80>(p, nb, st);
+    case 96: return launch_bwd_dq_d<T, 96>(p, nb, st);
     case 128: return launch_bwd_dq_d<T, 128>(p, nb, st);
     default: return hipErrorInvalidValue;
   }

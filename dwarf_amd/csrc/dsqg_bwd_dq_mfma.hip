@@ -36,15 +36,18 @@ namespace dsqg {
 constexpr int kDqTableStride = 48;
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC != 11) ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
+  using G_ = Geo<D>;
   constexpr int QT = 64;
-  constexpr int KS = D / 32;
-  constexpr int DB = D / 16;
-  constexpr int RV = D + 8;               // LDS row stride (36 dwords at D=64: conflict-free 16-byte row reads)
+  constexpr int KS = G_::KS;
+  constexpr int DB = G_::DB;
+  constexpr int RV = G_::RV;              // LDS row stride (36 dwords at D=64: conflict-free 16-byte row reads)
   constexpr int WIN = QT + kMaxWindow;
-  constexpr int CPR = D / 8;
-  constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
-  constexpr int CHW = D / 32;             // 16-byte chunks per lane of a wave's 16-row block
+  constexpr int CPR = G_::CPR;
+  constexpr int CPS = G_::CPS;            // chunks per staged (padded) row
+  constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
+  constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
+  constexpr int CPRP = G_::CPRP;          // lanes per row in the row-chunk layout
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   constexpr int PF = 2;                   // long-range K/V operands loaded ahead of use
   constexpr int TS = kDqTableStride;
@@ -103,10 +106,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
   int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
-    qlaneR[u] = opaque(rc_row<D>(l, u) * qsn + rc_chunk<D>(l, u) * 8);
-    olaneR[u] = opaque(rc_row<D>(l, u) * dosn + rc_chunk<D>(l, u) * 8);
-    klaneR[u] = opaque(rc_row<D>(l, u) * ksn + rc_chunk<D>(l, u) * 8);
-    vlaneR[u] = opaque(rc_row<D>(l, u) * vsn + rc_chunk<D>(l, u) * 8);
+    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
+    olaneR[u] = opaque(rc_lane<D>(l, u, dosn));
+    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
+    vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
   }
 
   for (int j = tid; j < J; j += kBlock) {
@@ -115,9 +118,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
     sGain[j] = gj;
   }
   if constexpr (HAS_SE) {
-    for (int e = tid; e < SEJ * D; e += kBlock) {
-      const int j = e / D, d = e - j * D;
-      split_bf16(j < J && p.scale_embed ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d],
+    constexpr int DP = G_::DP;
+    for (int e = tid; e < SEJ * DP; e += kBlock) {
+      const int j = e / DP, d = e - j * DP;
+      split_bf16(j < J && d < D && p.scale_embed ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d],
                  sSElo[j * RV + d]);
     }
   }
@@ -161,14 +165,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
 #pragma unroll
     for (int u = 0; u < CWIN; ++u) {
       const int ci = tid + u * kBlock;
-      wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque((ci / CPR) * ksn + (ci % CPR) * 8));
-      wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque((ci / CPR) * vsn + (ci % CPR) * 8));
+      const bool cv = ci % CPS < CPR;
+      wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
+      wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
     }
     bf16x8_t qB[KS], oB[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
-      oB[s] = as_bf16x8(bload16(rO, n0w * dosn + olane + 32 * s));
+      const bool sv = 8 * g + 32 * s < D;  // the zero columns of D = 80's last K-step
+      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (sv ? qlane + 32 * s : kNoElem)));
+      oB[s] = as_bf16x8(bload16(rO, n0w * dosn + (sv ? olane + 32 * s : kNoElem)));
     }
     uint4 qR[CHW], oR[CHW];
 #pragma unroll
@@ -195,9 +201,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
 #pragma unroll
     for (int u = 0; u < CWIN; ++u) {
       const int ci = tid + u * kBlock;
-      if (ci < WIN * CPR) {
-        st16(sK + (ci / CPR) * RV + (ci % CPR) * 8, wk[u]);
-        st16(sV + (ci / CPR) * RV + (ci % CPR) * 8, wv[u]);
+      if (ci < WIN * CPS) {
+        st16(sK + (ci / CPS) * RV + (ci % CPS) * 8, wk[u]);
+        st16(sV + (ci / CPS) * RV + (ci % CPS) * 8, wv[u]);
       }
     }
     __syncthreads();
@@ -310,18 +316,20 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
           const float qk = dot8_bf16(qR[u], kS[t % PF][u], 0.f);
-          const float dv = group_sum<CPR>(dot8_bf16(oR[u], vS[t % PF][u], 0.f));
-          st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
+          const float dv = group_sum<CPRP>(dot8_bf16(oR[u], vS[t % PF][u], 0.f));
+          if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
           if constexpr (HAS_SE) {
-            const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + rc_chunk<D>(l, u) * 8);
-            const uint4 sel = *reinterpret_cast<const uint4*>(sSElo + j * RV + rc_chunk<D>(l, u) * 8);
+            // Lanes past the row read chunk 0 (finite) against their zero query chunk.
+            const int sc8 = rc_valid<D>(l, u) ? rc_chunk<D>(l, u) * 8 : 0;
+            const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + sc8);
+            const uint4 sel = *reinterpret_cast<const uint4*>(sSElo + j * RV + sc8);
             const float qse = dot8_bf16(qR[u], sel, dot8_bf16(qR[u], se, 0.f));
-            const float sc = group_sum<CPR>(fmaf(c2, qse, sGain[j] * c2 * qk));
-            const float raw = g_grad ? group_sum<CPR>(qk) : 0.f;
+            const float sc = group_sum<CPRP>(fmaf(c2, qse, sGain[j] * c2 * qk));
+            const float raw = g_grad ? group_sum<CPRP>(qk) : 0.f;
             if (rc_chunk<D>(l, u) == 0)
               *reinterpret_cast<float4*>(sPair[w][rc_row<D>(l, u)]) = float4{sc, dv, raw, 0.f};
           } else {
-            const float dk = group_sum<CPR>(qk);
+            const float dk = group_sum<CPRP>(qk);
             if (rc_chunk<D>(l, u) == 0)
               *reinterpret_cast<float2*>(sPair[w][rc_row<D>(l, u)]) = float2{dk, dv};
           }
@@ -371,7 +379,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE && NSC != 11 ? 2 : 3
       // The wave's Q rows (natural order) replace its K rows, for dse after the tables are done.
       if (se_grad) {
 #pragma unroll
-        for (int u = 0; u < CHW; ++u) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
+        for (int u = 0; u < CHW; ++u)
+          if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
       }
     }
 
@@ -538,6 +547,8 @@ hipError_t launch_bwd_dq_mfma(const BwdParams& p, int D, unsigned nblocks, hipSt
   switch (D) {
     case 32: return launch_dq_mfma_d<32>(p, nblocks, st);
     case 64: return launch_dq_mfma_d<64>(p, nblocks, st);
+    case 80: return launch_dq_mfma_d<80>(p, nblocks, st);
+    case 96: return launch_dq_mfma_d<96>(p, nblocks, st);
     case 128: return launch_dq_mfma_d<128>(p, nblocks, st);
     default: return hipErrorInvalidValue;
   }

@@ -14,6 +14,11 @@ constexpr int kBlock = 256;       // threads per workgroup (4 wave64)
 
 typedef uint16_t bf16_t;
 
+// Lanes per row of the VALU kernels: D/8 (eight elements per lane) rounded up to a power of
+// two, so that a row's lanes form an aligned DPP group; for D = 80 and 96 (16 lanes) the lanes
+// past the row hold zeros and store nothing.
+constexpr int lanes_per_row(int D) { return D <= 32 ? 4 : (D <= 64 ? 8 : 16); }
+
 // ---------------------------------------------------------------------------------------
 // Element conversion.  bf16 is the upper half of an IEEE binary32; float -> bf16 rounds to
 // nearest-even (NaN stays a quiet NaN).

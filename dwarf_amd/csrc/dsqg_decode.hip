@@ -78,7 +78,7 @@ __device__ __forceinline__ void groups_scatter_sum(float (&a)[8]) {
 
 template <typename T, int D, int JMAX, bool HAS_SE>
 __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
-  constexpr int G = D / 8;
+  constexpr int G = lanes_per_row(D);  // lanes with 8g >= D (D = 80, 96) hold zeros
   constexpr int R = 64 / G;
   constexpr int P = (JMAX + R - 1) / R;
   constexpr int E = sizeof(T);
@@ -92,13 +92,14 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   const int b = (int)bh / p.H, h = (int)bh - b * p.H;  // B * H < 2^31 (checked by the ABI)
   const int r = lane / G, g = lane - r * G;
   const int d0 = g * 8;
+  const bool lane_ok = d0 < D;
   const int J = p.taps.J, S = p.S;
   const float c = p.scale;
   const long long pos = p.pos[b];
   T* outrow = static_cast<T*>(p.out) + bh * D;
   if (pos < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
     if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
-    if (lane < G) {
+    if (lane < G && lane_ok) {
       float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = __int_as_float(0x7fc00000);
@@ -126,9 +127,9 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   uint4 qraw[C16], knraw[C16], vnraw[C16];
 #pragma unroll
   for (int u = 0; u < C16; ++u) {
-    qraw[u] = ld16(qrow + d0 + 4 * u * (E == 4));
-    knraw[u] = ld16(knew + d0 + 4 * u * (E == 4));
-    vnraw[u] = ld16(vnew + d0 + 4 * u * (E == 4));
+    qraw[u] = lane_ok ? ld16(qrow + d0 + 4 * u * (E == 4)) : zero16();
+    knraw[u] = lane_ok ? ld16(knew + d0 + 4 * u * (E == 4)) : zero16();
+    vnraw[u] = lane_ok ? ld16(vnew + d0 + 4 * u * (E == 4)) : zero16();
   }
   float pbias[P], pgain[P];
 #pragma unroll
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   // Slot of tap delta: (pos mod S) - delta, wrapped once (0 < delta < S).  The new row goes
   // into slot pos mod S now: no tap of this step reads that slot.
   const int base = (pos >> 31) == 0 ? (int)pos % S : (int)(pos % S);  // 32-bit when it fits
-  if (r == 0) {
+  if (r == 0 && lane_ok) {
 #pragma unroll
     for (int u = 0; u < C16; ++u) {
       st16(kring + base * D + d0 + 4 * u * (E == 4), knraw[u]);
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     ok[t] = j < J && pos - dl >= 0;
     if (dl > 0) {
       const int sw = base - dl;
-      const unsigned off = ok[t] ? (unsigned)(((sw < 0 ? sw + S : sw) * D + d0) * E) : 0x80000000u;
+      const unsigned off = ok[t] && lane_ok ? (unsigned)(((sw < 0 ? sw + S : sw) * D + d0) * E) : 0x80000000u;
 #pragma unroll
       for (int u = 0; u < C16; ++u) {
         kraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rK, off + 16 * u, 0, 0));
@@ -189,8 +190,10 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     float part = pk * pgain[t];
     if constexpr (HAS_SE) {
       if constexpr (E == 2) Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
+      if (lane_ok) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[jj * D + d0 + e], part);
+        for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[jj * D + d0 + e], part);
+      }
     }
     const float tot = group_sum<G>(part);
     s[t] = ok[t] ? fmaf(tot, c, pbias[t]) : -INFINITY;
@@ -221,11 +224,13 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   const float inv = a / l;
   if constexpr (G == 16) {  // two elements per lane: 4 (lane>>5 & 1) + 2 (lane>>4 & 1) + {0,1}
     const int e0 = 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1);
-    if constexpr (E == 2) {
-      *reinterpret_cast<unsigned*>(outrow + d0 + e0) =
-          f32_to_bf16(acc[0] * inv) | (f32_to_bf16(acc[1] * inv) << 16);
-    } else {
-      *reinterpret_cast<float2*>(outrow + d0 + e0) = make_float2(acc[0] * inv, acc[1] * inv);
+    if (lane_ok) {
+      if constexpr (E == 2) {
+        *reinterpret_cast<unsigned*>(outrow + d0 + e0) =
+            f32_to_bf16(acc[0] * inv) | (f32_to_bf16(acc[1] * inv) << 16);
+      } else {
+        *reinterpret_cast<float2*>(outrow + d0 + e0) = make_float2(acc[0] * inv, acc[1] * inv);
+      }
     }
   } else if (G == 8 || (r & 1) == 0) {  // one element per lane (D = 32: both lanes of a pair hold it)
     const int e0 = (lane >> 3) & 7;
@@ -259,6 +264,8 @@ static hipError_t launch_decode_dtype(const DecodeParams& p, int D, hipStream_t 
   switch (D) {
     case 32: return launch_decode_d<T, 32>(p, st);
     case 64: return launch_decode_d<T, 64>(p, st);
+    case 80: return launch_decode_d<T, 80>(p, st);
+    case 96: return launch_decode_d<T, 96>(p, st);
     case 128: return launch_decode_d<T, 128>(p, st);
     default: return hipErrorInvalidValue;
   }

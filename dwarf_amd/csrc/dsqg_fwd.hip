@@ -2,8 +2,9 @@
 // (more than kMaxSparse taps beyond the dense window).
 //
 // One workgroup = one (b,h) and a tile of QPB query rows.  Each query row is owned by a group
-// of G = D/8 consecutive lanes, lane g holding elements [8g, 8g+8) of the row, so one row is
-// one coalesced D*sizeof(T)-byte access by the group.  The dense window (delta = 0..W) of K and
+// of G consecutive lanes (D/8 rounded up to a power of two), lane g holding elements
+// [8g, 8g+8) of the row (lanes with 8g >= D hold zeros), so one row is one coalesced
+// D*sizeof(T)-byte access by the group.  The dense window (delta = 0..W) of K and
 // V for the tile, rows [n0-W, n0+QPB), is staged in LDS once and reused by every row of the
 // tile; the long-range taps are gathered straight from global memory (the rows of tap delta
 // for the tile are the contiguous block [n0-delta, n0-delta+QPB)).  Scores are kept in
@@ -20,7 +21,7 @@ namespace dsqg {
 
 template <typename T, int D, int JMAX, bool HAS_SE>
 __global__ __launch_bounds__(kBlock) void fwd_valu_kernel(FwdParams p) {
-  constexpr int G = D / 8;
+  constexpr int G = lanes_per_row(D);
   constexpr int QPB = kBlock / G;
   constexpr int ROWS = QPB + kMaxWindow;
   constexpr int CPR = D * (int)sizeof(T) / 16;  // 16-byte chunks per row
@@ -66,10 +67,11 @@ __global__ __launch_bounds__(kBlock) void fwd_valu_kernel(FwdParams p) {
   const int n = n0 + qi;
   const bool row_ok = n < N;
   const int d0 = g * 8;
+  const bool lane_ok = d0 < D;  // lanes past the row (D = 80, 96) hold zeros
   const float c = p.scale;
 
   float q[8];
-  if (row_ok) {
+  if (row_ok && lane_ok) {
     Vec8<T>::load(qb + n * p.qs.n + d0, q);
   } else {
 #pragma unroll
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(kBlock) void fwd_valu_kernel(FwdParams p) {
       const int m = n - dl;
       const bool ok = row_ok && m >= 0;
       float part = 0.f;
-      if (ok) {
+      if (ok && lane_ok) {
         float kx[8];
         if (j <= W) Vec8<T>::load(sK + (m - base) * D + d0, kx);
         else Vec8<T>::load(kb + m * p.ks.n + d0, kx);
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(kBlock) void fwd_valu_kernel(FwdParams p) {
     if (j < J) {
       const float pj = __expf(s[j] - mx);
       l += pj;
-      if (pj > 0.f) {
+      if (pj > 0.f && lane_ok) {
         const int m = n - p.taps.delta[j];
         float vx[8];
         if (j <= W) Vec8<T>::load(sV + (m - base) * D + d0, vx);
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(kBlock) void fwd_valu_kernel(FwdParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = acc[e] * inv;
     T* ob = static_cast<T*>(p.out) + b * p.os.b + h * p.os.h + n * p.os.n + d0;
-    Vec8<T>::store(ob, o);
+    if (lane_ok) Vec8<T>::store(ob, o);
     if (p.lse && g == 0) p.lse[((long long)b * p.H + h) * N + n] = mx + __logf(l);
   }
 }
@@ -143,7 +145,7 @@ __global__ __launch_bounds__(kBlock) void fwd_valu_kernel(FwdParams p) {
 template <typename T, int D, int JMAX>
 static hipError_t launch_fwd_t(const FwdParams& p0, hipStream_t st) {
   FwdParams p = p0;
-  constexpr int QPB = kBlock / (D / 8);
+  constexpr int QPB = kBlock / lanes_per_row(D);
   p.n_tiles = (p.N + QPB - 1) / QPB;
   const long long nblocks = (long long)p.B * p.H * p.n_tiles;
   if (nblocks == 0) return hipSuccess;
@@ -164,6 +166,8 @@ static hipError_t launch_fwd_dtype(const FwdParams& p, int D, hipStream_t st) {
   switch (D) {
     case 32: return launch_fwd_d<T, 32>(p, st);
     case 64: return launch_fwd_d<T, 64>(p, st);
+    case 80: return launch_fwd_d<T, 80>(p, st);
+    case 96: return launch_fwd_d<T, 96>(p, st);
     case 128: return launch_fwd_d<T, 128>(p, st);
     default: return hipErrorInvalidValue;
   }

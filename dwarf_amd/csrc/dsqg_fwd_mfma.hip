@@ -35,16 +35,17 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4)) void fwd_mfma_kernel(FwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC != 11 ? 3 : 4))) void fwd_mfma_kernel(FwdParams p) {
+  using G_ = Geo<D>;
   constexpr int QT = 64;                  // query rows per workgroup
-  constexpr int KS = D / 32;              // 16x16x32 steps over the head dim
-  constexpr int DB = D / 16;              // 16-wide head-dim blocks of the output
-  constexpr int RV = D + 8;               // LDS row stride of the K / V tiles (36 dwords at D=64)
+  constexpr int KS = G_::KS;              // 16x16x32 steps over the head dim
+  constexpr int DB = G_::DB;              // 16-wide head-dim blocks of the output
+  constexpr int RV = G_::RV;              // LDS row stride of the K / V tiles (36 dwords at D=64)
   constexpr int WIN = QT + kMaxWindow;    // dense-window rows of V staged in LDS
-  constexpr int CPR = D / 8;              // 16-byte chunks per row
-  constexpr int CWIN = (WIN * CPR + kBlock - 1) / kBlock;
-  constexpr int CHW = 16 * CPR / 64;      // chunks per lane of a wave's 16-row block
-  static_assert(16 * CPR % 64 == 0, "a wave's 16-row block must split evenly over 64 lanes");
+  constexpr int CPR = G_::CPR;            // 16-byte chunks per row
+  constexpr int CPS = G_::CPS;            // ... per staged row (zero chunks pad D = 80 to 96)
+  constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
+  constexpr int CHW = G_::CHW;            // chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
 #ifdef DSQG_FWD_PF
   constexpr int PF = DSQG_FWD_PF;
@@ -93,21 +94,23 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
-    wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque((ci / CPR) * vsn + (ci % CPR) * 8));
-    wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque((ci / CPR) * ksn + (ci % CPR) * 8));
+    const bool cv = ci % CPS < CPR;
+    wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
+    wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
   }
   const int qlane = opaque(i * qsn + 8 * g);
   bf16x8_t qB[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + qlane + 32 * s));
+  for (int s = 0; s < KS; ++s)
+    qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (8 * g + 32 * s < D ? qlane + 32 * s : kNoElem)));
   // The same query rows and the long-range key rows n0w - delta + 0..15 in the row-chunk
   // layout (whole rows per 8 lanes); the keys in two halves (the second after the dense band has
   // consumed its registers) to bound the register peak.
   int qlaneR[CHW], klaneR[CHW];
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
-    qlaneR[u] = opaque(rc_row<D>(l, u) * qsn + rc_chunk<D>(l, u) * 8);
-    klaneR[u] = opaque(rc_row<D>(l, u) * ksn + rc_chunk<D>(l, u) * 8);
+    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
+    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
   }
   uint4 qR[CHW];
 #pragma unroll
@@ -134,9 +137,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
     // fp32 precision to about 2^-17.
     bf16_t* const sSE = sK;
     bf16_t* const sSElo = sV;
-    for (int e = tid; e < 48 * D; e += kBlock) {
-      const int j = e / D, d = e - j * D;
-      split_bf16(j < J ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d], sSElo[j * RV + d]);
+    constexpr int DP = G_::DP;
+    for (int e = tid; e < 48 * DP; e += kBlock) {
+      const int j = e / DP, d = e - j * DP;
+      split_bf16(j < J && d < D ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d], sSElo[j * RV + d]);
     }
     __syncthreads();
 #pragma unroll
@@ -160,8 +164,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
-    const int r = ci / CPR, cc = ci - r * CPR;
-    if (ci < WIN * CPR) {
+    const int r = ci / CPS, cc = ci - r * CPS;
+    if (ci < WIN * CPS) {
       st16(sV + r * RV + cc * 8, wv[u]);
       st16(sK + r * RV + cc * 8, wk[u]);
     }
@@ -190,7 +194,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
     for (int u = 0; u < CHW; ++u) {
       float d = sGain2[j] * dot8_bf16(qR[u], kS[t][u], 0.f);
-      d = group_sum<CPR>(d);
+      d = group_sum<G_::CPRP>(d);
       if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * TR + t] = d;
     }
   };
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   }
   int vlane[CHW];  // this lane's chunks of a wave's 16-row V block (row-chunk layout)
 #pragma unroll
-  for (int u = 0; u < CHW; ++u) vlane[u] = opaque(rc_row<D>(l, u) * vsn + rc_chunk<D>(l, u) * 8);
+  for (int u = 0; u < CHW; ++u) vlane[u] = opaque(rc_lane<D>(l, u, vsn));
   uint4 vS[PF][CHW];  // long-range V rows n0w - delta + 0..15, PF taps ahead
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
@@ -296,7 +300,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
 #pragma unroll
-      for (int u = 0; u < CHW; ++u) st16(sSt + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, vS[t % PF][u]);
+      for (int u = 0; u < CHW; ++u)
+        if (rc_valid<D>(l, u)) st16(sSt + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, vS[t % PF][u]);
       if (t + PF < NS) {
         const int r0 = n0w - dl_s[t + PF];
 #pragma unroll
@@ -324,7 +329,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (HAS_SE || NSC != 11 ? 3 : 4
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
     const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
-    if (n0w + rr < N)
+    if (n0w + rr < N && cc < CPR)
       st16(outb + (n0w + rr) * p.os.n + 8 * cc, *reinterpret_cast<const uint4*>(sSt + rr * RV + 8 * cc));
   }
 }
@@ -358,7 +363,7 @@ bool fwd_mfma_supported(const FwdParams& p, int D) {
   const long long rmin = p.qs.n < p.ks.n ? (p.qs.n < p.vs.n ? p.qs.n : p.vs.n)
                                           : (p.ks.n < p.vs.n ? p.ks.n : p.vs.n);
   const long long span = ((long long)p.N + p.taps.maxd + 64) * rs * 2;
-  return (D == 32 || D == 64 || D == 128) && p.taps.J - p.taps.W - 1 <= kMaxSparse &&
+  return (D == 32 || D == 64 || D == 80 || D == 96 || D == 128) && p.taps.J - p.taps.W - 1 <= kMaxSparse &&
          rmin >= D && span < (1LL << 31);
 }
 
@@ -366,6 +371,8 @@ hipError_t launch_fwd_mfma(const FwdParams& p, int D, hipStream_t st) {
   switch (D) {
     case 32: return launch_fwd_mfma_d<32>(p, st);
     case 64: return launch_fwd_mfma_d<64>(p, st);
+    case 80: return launch_fwd_mfma_d<80>(p, st);
+    case 96: return launch_fwd_mfma_d<96>(p, st);
     case 128: return launch_fwd_mfma_d<128>(p, st);
     default: return hipErrorInvalidValue;
   }

@@ -58,15 +58,48 @@ __device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
   return acc;
 }
 
-// Row-chunk layout of a wave's 16-row block of a [rows][D] bf16 matrix: load u (0 .. D/32-1)
-// gives lane l the 16-byte chunk (l + 64u) % (D/8) of row (l + 64u) / (D/8).  Eight (D=64)
+// Head-dim geometry of the bf16 MFMA kernels; D is a multiple of 16 in [32, 128].
+//  * The MFMA K-steps cover DP = D rounded up to 32.  For D = 80 the 16 extra columns are zero
+//    in every operand (loaded as zeros, staged as zeros).
+//  * A row is CPR = D/8 16-byte chunks.  The row-chunk layout (below) spreads a row over CPRP
+//    lanes, CPR rounded up to a power of two, so that DPP sums run over aligned lane groups;
+//    lanes whose chunk is >= CPR carry zeros and store nothing.
+template <int D>
+struct Geo {
+  static_assert(D % 16 == 0 && D >= 32 && D <= 128, "head dim");
+  static constexpr int DP = (D + 31) / 32 * 32;
+  static constexpr int KS = DP / 32;        // 16x16x32 K-steps over the head dim
+  static constexpr int DB = D / 16;         // 16-wide head-dim blocks of an output
+  static constexpr int CPR = D / 8;         // 16-byte chunks of a row
+  static constexpr int CPS = DP / 8;        // ... of a staged (padded) LDS row
+  static constexpr int CPRP = CPR <= 4 ? 4 : (CPR <= 8 ? 8 : 16);
+  static constexpr int CHW = 16 * CPRP / 64;  // chunks per lane of a wave's 16-row block
+  static constexpr int RV = DP + 8;         // LDS row stride (elements)
+};
+
+// Row-chunk layout of a wave's 16-row block of a [rows][D] bf16 matrix: load u (0 .. CHW-1)
+// gives lane l the 16-byte chunk (l + 64u) % CPRP of row (l + 64u) / CPRP.  Eight (D=64)
 // consecutive lanes then read one whole 128-byte row, which the vector L1 serves at close to
 // four times the rate of the MFMA operand order (16 rows x 16 bytes per 16 lanes), where every
 // group of four lanes touches four different cache lines.
 template <int D>
-__device__ __forceinline__ int rc_row(int l, int u) { return (l + 64 * u) / (D / 8); }
+__device__ __forceinline__ int rc_row(int l, int u) { return (l + 64 * u) / Geo<D>::CPRP; }
 template <int D>
-__device__ __forceinline__ int rc_chunk(int l, int u) { return (l + 64 * u) % (D / 8); }
+__device__ __forceinline__ int rc_chunk(int l, int u) { return (l + 64 * u) % Geo<D>::CPRP; }
+template <int D>
+__device__ __forceinline__ bool rc_valid(int l, int u) { return rc_chunk<D>(l, u) < Geo<D>::CPR; }
+
+// An element offset that a slice's buffer resource turns into zeros when added to any row
+// offset a kernel forms: with (N + max offset + 64) * rs * 2 < 2^31 (checked at launch), every
+// row offset r * rs lies in (-2^30, 2^30), so r * rs + kNoElem is past the slice's end.
+constexpr int kNoElem = 1 << 30;
+
+// This lane's element offset in the row-chunk layout of a block with row stride rs, or
+// kNoElem for a lane past the row (its loads then read zeros).
+template <int D>
+__device__ __forceinline__ int rc_lane(int l, int u, int rs) {
+  return rc_valid<D>(l, u) ? rc_row<D>(l, u) * rs + rc_chunk<D>(l, u) * 8 : kNoElem;
+}
 
 // Buffer resource over one (b,h) slice of a [B,H,N,D] bf16 operand: rows [0, N) of row stride rs
 // elements.  Raw buffer loads range-check each access against the slice size, so a row below 0
@@ -81,7 +114,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const bf16_t* base,
 
 // 16 bytes at element offset `elem` of a buffer (zero when out of range).
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int elem) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (unsigned)(elem * 2), 0, 0));
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (unsigned)elem * 2u, 0, 0));
 }
 
 // Hides a per-lane value from the optimiser, so that (uniform row) * stride + lane_part is not

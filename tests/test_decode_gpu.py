@@ -64,7 +64,7 @@ def test_decode_workload_1000_steps(gpu_device):
     assert torch.equal(d["v_ring"].cpu(), v_ring_ref)
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 80, 96, 128])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("p", [0, 7, 40, 1535, 1536, 2500])
 def test_decode_equals_full_sequence_row(gpu_device, dtype, p, D):

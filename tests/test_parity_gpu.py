@@ -119,7 +119,7 @@ def test_config0_fp32_forward(gpu_device):
     compare(got, ref, "fp32")
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 80, 96, 128])
 def test_fp32_fwd_bwd_all_parameters(gpu_device, D):
     inp = _rand_inputs(2, 3, 1700, D, OFFSETS_V3, torch.float32, seed=100 + D)
     _say(f"fp32 fwd+bwd B2 H3 N1700 D{D} with se, g, a")
@@ -209,13 +209,45 @@ def test_bf16_table_beyond_the_mfma_kernels_is_rejected(gpu_device):
     compare(got, ref, "fp32")
 
 
-@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("D", [32, 64, 80, 96, 128])
 def test_bf16_head_dims_all_parameters(gpu_device, D):
     inp = _rand_inputs(2, 3, 1700, D, OFFSETS_V3, torch.bfloat16, seed=200 + D)
     _say(f"bf16 fwd+bwd B2 H3 N1700 D{D} with se, g, a")
     got = gpu_run(inp, OFFSETS_V3, gpu_device)
     ref = oracle_chunked(inp, OFFSETS_V3, torch.float32)
     compare(got, ref, "bf16")
+
+
+def test_85m_condu_trainer_shape_d96(gpu_device):
+    """train/train_2048_85m_condU.py:60-62 builds E 768 with H 8 (HD 96) and calls
+    dsqg_attention_v3(q, k, v, pos_bias, scale_embed) (:112-115, 169): B8 H8 N2048 D96."""
+    inp = _rand_inputs(8, 8, 2048, 96, OFFSETS_V3, torch.bfloat16, seed=96, gains=False)
+    inp["scale_embed"] = inp["scale_embed"] * 0.5          # ~0.05 N(0,1), as the reference's tests
+    _say("85M condU trainer shape B8 H8 N2048 D96 with scale_embed")
+    got = gpu_run(inp, OFFSETS_V3, gpu_device)
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float32)
+    compare(got, ref, "bf16", case="85M condU B8 H8 N2048 D96 + scale_embed")
+
+
+def test_v2_self_test_85m_shape_d80(gpu_device):
+    """kernels/dsqg_attention_v2.py:508-513, "85M shape (HD=80)": (4, 8, 2047, 80), seed 42,
+    q/k/v ~ 0.1 N(0,1) drawn in bf16, pos_bias ~ 0.5 N(0,1), no scale_embed, gradient of
+    out.sum(); the reference passes at 0.05 absolute."""
+    B, H, N, D = 4, 8, 2047, 80
+    torch.manual_seed(42)
+    q = torch.randn(B, H, N, D, dtype=torch.bfloat16) * 0.1
+    k = torch.randn(B, H, N, D, dtype=torch.bfloat16) * 0.1
+    v = torch.randn(B, H, N, D, dtype=torch.bfloat16) * 0.1
+    pb = torch.randn(44, H, dtype=torch.float32) * 0.5
+    dev = gpu_device
+    qd, kd, vd = (t.to(dev).requires_grad_(True) for t in (q, k, v))
+    out = dwarf_amd.dsqg_attention_v2(qd, kd, vd, pb.to(dev))
+    out.float().sum().backward()
+    torch.cuda.synchronize(dev)
+    got = {"out": out.detach().cpu(), "dq": qd.grad.cpu(), "dk": kd.grad.cpu(), "dv": vd.grad.cpu()}
+    ref = dsqg_forward_backward(q, k, v, pb, torch.ones(B, H, N, D), None, dtype=torch.float32)
+    errs = compare(got, ref, "bf16", keys=("out", "dq", "dk", "dv"), case="V2 self-test (4, 8, 2047, 80)")
+    assert max(e for e, _ in errs.values()) < 0.05
 
 
 def test_empty_inputs(gpu_device):
