@@ -113,47 +113,83 @@ def cpu_baseline_decode(steps=10):
             "ms_per_step": round(dt * 1e3, 3)}
 
 
-def bench_decode(dev, steps=1000):
+def bench_decode(dev, steps=1000, layers=8):
+    """Ring-buffer decode step, workload 4 (B256 H12 D64, 44 offsets, 1537-slot rings).
+
+    Two figures, both from HIP-graph replays timed with HIP events:
+    * ``layers`` (the headline): ``layers`` independent ring pairs, as the caches of an
+      8-layer model (8 x 1.2 GB), each token stepping every layer once.  A layer's rows come
+      back only after the other layers' steps (8 x 36 MB > the 256 MB Infinity Cache), so the
+      bytes come from HBM.
+    * ``single_ring``: ``steps`` consecutive steps on one ring pair, where a step re-reads the
+      dense-window rows the previous step read (cache-assisted; kept for comparison).
+    """
     import torch
     from dwarf_amd import ops
     from dwarf_amd.workloads import DECODE, decode_bytes_per_step, make_decode_inputs
     cfg = DECODE
-    d = make_decode_inputs(device=dev)
-    pos_a = d["pos"].clone()
-    pos_b = torch.empty_like(pos_a)
-    out = torch.empty_like(d["q"])
+    B, H, D, S = cfg["B"], cfg["H"], cfg["D"], cfg["S"]
     offs = list(cfg["offsets"])
+    small = make_decode_inputs(device="cpu", B=B, H=H, D=D, S=2)  # q, k_new, v_new, pos, bias
+    gen = torch.Generator(device=dev).manual_seed(4004)
+    sets = []
+    for _ in range(layers):
+        ring = lambda: torch.randn((B, H, S, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        rows = lambda: torch.randn((B, H, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        pos_a = small["pos"].to(dev)
+        sets.append(dict(k_ring=ring(), v_ring=ring(), q=rows(), k_new=rows(), v_new=rows(),
+                         pos_a=pos_a, pos_b=torch.empty_like(pos_a),
+                         out=torch.empty((B, H, D), device=dev, dtype=torch.bfloat16)))
+    pb = small["pos_bias"].to(dev)
 
-    def step(src, dst):
-        ops.decode_step_into(d["q"], d["k_new"], d["v_new"], d["k_ring"], d["v_ring"], src,
-                             d["pos_bias"], None, None, None, offs, out, dst)
+    def step(d, flip):
+        src, dst = (d["pos_a"], d["pos_b"]) if not flip else (d["pos_b"], d["pos_a"])
+        ops.decode_step_into(d["q"], d["k_new"], d["v_new"], d["k_ring"], d["v_ring"], src, pb,
+                             None, None, None, offs, d["out"], dst)
 
-    s = torch.cuda.Stream(dev)
-    s.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(s):
-        for i in range(4):
-            step(pos_a, pos_b) if i % 2 == 0 else step(pos_b, pos_a)
-    torch.cuda.current_stream(dev).wait_stream(s)
-    torch.cuda.synchronize(dev)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
-        for i in range(steps):
-            step(pos_a, pos_b) if i % 2 == 0 else step(pos_b, pos_a)
-    graph.replay()  # warm-up replay
-    torch.cuda.synchronize(dev)
-    st = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    graph.replay()
-    e1.record(st)
-    e1.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / steps
-    nbytes = decode_bytes_per_step(cfg["B"], cfg["H"], cfg["D"], len(offs))
-    gbs = nbytes / (us * 1e-6) / 1e9
-    return {"workload": "decode B256 H12 D64 J44 ring 1537 (config 4)", "steps": steps,
-            "us_per_step": round(us, 3), "tok_per_s": round(cfg["B"] / (us * 1e-6), 1),
-            "algorithmic_bytes_per_step": nbytes, "achieved_GBs": round(gbs, 1),
-            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "timing": "hipGraph replay, HIP events"}
+    def timed_graph(order):
+        s = torch.cuda.Stream(dev)
+        s.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(s):
+            for i in range(4):
+                for li, flip in order[:2 * layers]:
+                    step(sets[li], flip)
+        torch.cuda.current_stream(dev).wait_stream(s)
+        torch.cuda.synchronize(dev)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for li, flip in order:
+                step(sets[li], flip)
+        graph.replay()  # warm-up replay
+        torch.cuda.synchronize(dev)
+        st = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        graph.replay()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / len(order)
+
+    tokens = max(1, steps // layers)
+    # Token t steps layer 0..layers-1, each layer flipping its own pos / pos_next pair.
+    us_layers = timed_graph([(li, t % 2 == 1) for t in range(tokens) for li in range(layers)])
+    us_single = timed_graph([(0, i % 2 == 1) for i in range(steps)])
+    nbytes = decode_bytes_per_step(B, H, D, len(offs))
+
+    def fig(us):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"us_per_step": round(us, 3), "tok_per_s": round(B / (us * 1e-6), 1),
+                "achieved_GBs": round(gbs, 1), "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    res = {"workload": f"decode B{B} H{H} D{D} J{len(offs)} ring {S} (config 4)",
+           "algorithmic_bytes_per_step": nbytes,
+           **fig(us_layers),
+           "layers": {"ring_pairs": layers, "tokens": tokens, "steps": tokens * layers,
+                      **fig(us_layers)},
+           "single_ring": {"steps": steps, **fig(us_single)},
+           "timing": "hipGraph replay, HIP events; headline figures are the layers variant"}
+    del sets
+    torch.cuda.empty_cache()
+    return res
 
 
 def bench_module(dev, steps=20, warmup=20):
@@ -302,11 +338,45 @@ def measured_traffic(kernel):
     return None
 
 
+def profile_decode(args, dev):
+    """Counter mode for the decode kernel: --profile-reps steps on each of 8 ring pairs in turn
+    (as the layers variant of the decode leg), then the plain copy of known size."""
+    import torch
+    from dwarf_amd import ops
+    from dwarf_amd.workloads import DECODE, make_decode_inputs
+    B, H, D, S = DECODE["B"], DECODE["H"], DECODE["D"], DECODE["S"]
+    small = make_decode_inputs(device="cpu", B=B, H=H, D=D, S=2)
+    gen = torch.Generator(device=dev).manual_seed(4004)
+    pb = small["pos_bias"].to(dev)
+    layers = []
+    for _ in range(8):
+        r = lambda *shp: torch.randn(shp, generator=gen, device=dev, dtype=torch.bfloat16)
+        layers.append((r(B, H, S, D), r(B, H, S, D), r(B, H, D), r(B, H, D), r(B, H, D),
+                       small["pos"].to(dev), torch.empty((B, H, D), device=dev, dtype=torch.bfloat16)))
+    for rep in range(args.profile_reps):
+        for kr, vr, q, kn, vn, pos, out in layers:
+            nxt = pos + 1
+            ops.decode_step_into(q, kn, vn, kr, vr, pos, pb, None, None, None,
+                                 list(DECODE["offsets"]), out, nxt)
+            pos.copy_(nxt)
+    nbytes = args.copy_mib << 20
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.profile_reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] profile mode: {8 * args.profile_reps} decode steps over 8 ring pairs, "
+          f"{args.profile_reps} copies of {nbytes} bytes", file=sys.stderr, flush=True)
+    return 0
+
+
 def profile_mode(args, w, dev):
     """Launches one kernel of the workload a few times and a plain copy of known size."""
     import torch
     from dwarf_amd import ops
     from dwarf_amd.workloads import make_inputs
+    if args.profile_kernel == "decode":
+        return profile_decode(args, dev)
     inp = make_inputs(w, device="cpu", seed=w.seed)
     d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
     fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
@@ -334,6 +404,94 @@ def profile_mode(args, w, dev):
     return 0
 
 
+def make_sets(w, dev, n, scale_embed=False, if_gain=False):
+    """`n` input sets of workload w (seeds w.seed + 100 i), each with its launch objects.
+    scale_embed / if_gain add the reference module's parameters (se ~ 0.05 N(0,1),
+    a ~ U(0.8, 1.2)), the call of train/train_2048_condU.py:184,187."""
+    import torch
+    from dwarf_amd import ops
+    from dwarf_amd.workloads import make_inputs
+    sets = []
+    for i in range(n):
+        inp = make_inputs(w, device="cpu", seed=w.seed + 100 * i)
+        g = torch.Generator().manual_seed(w.seed + 100 * i + 7)
+        if scale_embed:
+            inp["scale_embed"] = torch.randn(w.J, w.D, generator=g) * 0.05
+        if if_gain:
+            inp["if_gain"] = torch.rand(w.H, generator=g) * 0.4 + 0.8
+        d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+        fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
+                           d["score_gain"], d["if_gain"], list(w.offsets))
+        bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
+                           d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
+                           d["scale_embed"] is not None, d["score_gain"] is not None,
+                           d["if_gain"] is not None)
+        sets.append((inp if i == 0 else None, d, fl, bl))
+    return sets
+
+
+def run_step(sets, i):
+    _, _, fl, bl = sets[i % len(sets)]
+    fl.run()
+    bl.run()
+
+
+def ramp(fn, ms):
+    """Calls fn(i) until `ms` milliseconds of wall time have passed; returns the call count."""
+    import torch
+    t0 = time.perf_counter()
+    i = 0
+    while (time.perf_counter() - t0) * 1000.0 < ms:
+        fn(i)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return i
+
+
+def kernel_bytes(w):
+    """Algorithmic bytes per launch: forward 4TDE+4T, dq 5TDE+8T, dk/dv 6TDE+8T."""
+    T, E = w.B * w.H * w.N, 2
+    return {"dsqg_fwd": w.fwd_bytes(), "dsqg_bwd_dq": 5 * T * w.D * E + 8 * T,
+            "dsqg_bwd_dkdv": 6 * T * w.D * E + 8 * T, "dsqg_bwd_params": None}
+
+
+def time_fwd_bwd(sets, steps, warmup, stream):
+    """W untimed steps, then K timed steps (median of per-step HIP events); then the per-kernel
+    launch durations inside the step's own order (fwd, dq, dk/dv, params, rotating the sets),
+    so every kernel meets the caches the step leaves it: a HIP event after each launch, median
+    over the steps.  (A full backward runs the parameter reduction inside the dk/dv launch; here
+    the phases are launched one by one.)  Returns (ms per step, {kernel: {us}}, wall ms)."""
+    import torch
+    for i in range(warmup):
+        run_step(sets, i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms = _events_ms(lambda i: run_step(sets, i), steps, stream)
+    wall = (time.perf_counter() - t0) * 1000.0 / steps
+    torch.cuda.synchronize()
+    names = ("dsqg_fwd", "dsqg_bwd_dq", "dsqg_bwd_dkdv", "dsqg_bwd_params")
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(steps)]
+    for i in range(steps):
+        _, _, fl, bl = sets[i % len(sets)]
+        ev[i][0].record(stream)
+        fl.run()
+        ev[i][1].record(stream)
+        bl.run("dq")
+        ev[i][2].record(stream)
+        bl.run("dkdv")
+        ev[i][3].record(stream)
+        bl.run("params")
+        ev[i][4].record(stream)
+    torch.cuda.synchronize()
+    per = {}
+    for k, name in enumerate(names):
+        us = statistics.median(ev[i][k].elapsed_time(ev[i][k + 1]) for i in range(steps)) * 1000.0
+        per[name] = {"us": round(us, 3)}
+    return ms, per, wall
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,13 +500,17 @@ def main(argv=None):
                     help="untimed steps first (the GPU clocks ramp during the first ~20 ms of work)")
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3])
     ap.add_argument("--sets", type=int, default=3, help="input sets rotated between steps")
+    ap.add_argument("--ramp-ms", type=float, default=150.0,
+                    help="untimed steps for this long before the warm-up (GPU clock ramp)")
+    ap.add_argument("--no-scale-embed-leg", action="store_true",
+                    help="skip the leg with scale_embed and IF gain (the reference module's call)")
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
     ap.add_argument("--no-pool", action="store_true", help="skip the interference-pool leg")
     ap.add_argument("--no-generation", action="store_true", help="skip the generation leg")
-    ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv"], default=None,
+    ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv", "decode"], default=None,
                     help="counter-collection mode: launch only this kernel --profile-reps times, "
                          "plus a plain device copy of --copy-mib MiB (the scale reference for "
                          "FETCH_SIZE / WRITE_SIZE), then exit without a JSON line")
@@ -372,71 +534,27 @@ def main(argv=None):
         return 1
     dev = torch.device("cuda:0")
     w = WORKLOADS[args.config]
-    T = w.B * w.H * w.N
-    E = 2
     print(f"[bench] config {w.index}: B{w.B} H{w.H} N{w.N} D{w.D} J{w.J} {w.dtype}, "
           f"{args.sets} input sets, warmup {args.warmup}, steps {args.steps}", file=sys.stderr, flush=True)
 
     if args.profile_kernel:
         return profile_mode(args, w, dev)
 
-    sets = []
-    for i in range(args.sets):
-        inp = make_inputs(w, device="cpu", seed=w.seed + 100 * i)
-        d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
-        fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
-                           d["score_gain"], d["if_gain"], list(w.offsets))
-        bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
-                           d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
-                           d["scale_embed"] is not None, d["score_gain"] is not None,
-                           d["if_gain"] is not None)
-        sets.append((inp if i == 0 else None, d, fl, bl))
+    sets = make_sets(w, dev, args.sets)
 
-    def step(i):
-        _, _, fl, bl = sets[i % len(sets)]
-        fl.run()
-        bl.run()
-
+    # GPU clock ramp: untimed steps until at least --ramp-ms of wall time have passed (the
+    # clocks rise over the first tens of milliseconds of work), then the W warm-up steps.
     stream = torch.cuda.current_stream(dev)
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ms = _events_ms(step, args.steps, stream)
-    wall = (time.perf_counter() - t0) * 1000.0 / args.steps
-    torch.cuda.synchronize()
-    print(f"[bench] fwd+bwd {ms:.4f} ms/step (wall {wall:.4f})", file=sys.stderr, flush=True)
-
-    # Per-kernel launch durations inside the step's own order (fwd, dq, dk/dv, params; rotating
-    # the sets), so every kernel meets the caches the step leaves it: a HIP event after each
-    # launch, median over the steps.  (A full backward runs the parameter reduction inside the
-    # dk/dv launch; here the phases are launched one by one.)
-    names = ("dsqg_fwd", "dsqg_bwd_dq", "dsqg_bwd_dkdv", "dsqg_bwd_params")
-    nbytes_of = {"dsqg_fwd": w.fwd_bytes(), "dsqg_bwd_dq": 5 * T * w.D * E + 8 * T,
-                 "dsqg_bwd_dkdv": 6 * T * w.D * E + 8 * T, "dsqg_bwd_params": None}
-    reps = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)] for _ in range(reps)]
-    torch.cuda.synchronize()
-    for i in range(reps):
-        _, _, fl, bl = sets[i % len(sets)]
-        ev[i][0].record(stream)
-        fl.run()
-        ev[i][1].record(stream)
-        bl.run("dq")
-        ev[i][2].record(stream)
-        bl.run("dkdv")
-        ev[i][3].record(stream)
-        bl.run("params")
-        ev[i][4].record(stream)
-    torch.cuda.synchronize()
-    per = {}
-    for k, name in enumerate(names):
-        us = statistics.median(ev[i][k].elapsed_time(ev[i][k + 1]) for i in range(reps)) * 1000.0
-        per[name] = {"us": round(us, 3)}
+    ramp_steps = ramp(lambda i: run_step(sets, i), args.ramp_ms)
+    ms, per, wall = time_fwd_bwd(sets, args.steps, args.warmup, stream)
+    print(f"[bench] fwd+bwd {ms:.4f} ms/step (wall {wall:.4f}; clock ramp {ramp_steps} steps)",
+          file=sys.stderr, flush=True)
+    nbytes_of = kernel_bytes(w)
+    for name in per:
         if nbytes_of[name]:
             per[name]["algorithmic_bytes"] = nbytes_of[name]
-            per[name]["achieved_GBs"] = round(nbytes_of[name] / (us * 1e-6) / 1e9, 1)
-        print(f"[bench] {name}: {us:.2f} us/launch", file=sys.stderr, flush=True)
+            per[name]["achieved_GBs"] = round(nbytes_of[name] / (per[name]["us"] * 1e-6) / 1e9, 1)
+        print(f"[bench] {name}: {per[name]['us']:.2f} us/launch", file=sys.stderr, flush=True)
     dom = max((k for k in per if "algorithmic_bytes" in per[k]), key=lambda k: per[k]["us"])
     achieved = per[dom]["achieved_GBs"]
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -459,9 +577,28 @@ def main(argv=None):
         "roofline": roofline,
         "kernels": per,
     }
+    if not args.no_scale_embed_leg:
+        # The reference module's call (train/train_2048_condU.py:184,187): config-2 shapes with
+        # scale_embed and IF gain, same protocol; its own step fraction of the HBM roofline.
+        se_sets = make_sets(w, dev, args.sets, scale_embed=True, if_gain=True)
+        ramp(lambda i: run_step(se_sets, i), args.ramp_ms / 3)
+        se_ms, se_per, _ = time_fwd_bwd(se_sets, args.steps, args.warmup, stream)
+        for name in se_per:
+            if nbytes_of[name]:
+                se_per[name]["achieved_GBs"] = round(nbytes_of[name] / (se_per[name]["us"] * 1e-6) / 1e9, 1)
+        result["scale_embed_leg"] = {
+            "workload": f"config {w.index} + scale_embed [J,D] ~ 0.05 N(0,1) + if_gain [H] ~ U(0.8,1.2)",
+            "ms_per_step": round(se_ms, 5), "tok_per_s": round(w.B * w.N / (se_ms * 1e-3), 1),
+            "fwd_bwd_frac_hbm_peak": round(step_bytes / (se_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernels": se_per}
+        print(f"[bench] scale_embed leg {se_ms:.4f} ms/step", file=sys.stderr, flush=True)
+        del se_sets
     if not args.no_decode:
         result["decode"] = bench_decode(dev, args.decode_steps)
-        print(f"[bench] decode {result['decode']['us_per_step']} us/step", file=sys.stderr, flush=True)
+        print(f"[bench] decode {result['decode']['us_per_step']} us/step over "
+              f"{result['decode']['layers']['ring_pairs']} ring pairs "
+              f"(single ring {result['decode']['single_ring']['us_per_step']})",
+              file=sys.stderr, flush=True)
     if not args.no_module:
         result["module"] = bench_module(dev)
         print(f"[bench] module QW fwd+bwd {result['module']['ms_per_step_strided_views']} ms "
