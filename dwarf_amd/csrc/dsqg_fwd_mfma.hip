@@ -35,7 +35,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC != 11 ? 3 : 4))) void fwd_mfma_kernel(FwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3 : 4))) void fwd_mfma_kernel(FwdParams p) {
   using G_ = Geo<D>;
   constexpr int QT = 64;                  // query rows per workgroup
   constexpr int KS = G_::KS;              // 16x16x32 steps over the head dim
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC
 #else
   constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
 #endif
-  constexpr int TS = 50;                  // row stride of the per-wave T table (every tap j < 48)
+  constexpr int TS = 49;                  // row stride of the per-wave T table (every tap j < 48; odd: rows on distinct banks)
   constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
   constexpr int TR = NSM + (NSM & 1);     // row stride of the long-range score table (distinct banks)
   constexpr float kLog2e = 1.4426950408889634f;
@@ -62,7 +62,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC
   // Wave-private staging block (16 rows x RV): the T table (scale_embed), then each long-range
   // tap's V rows, then the output rows.
   __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : 16 * RV];
-  __shared__ __align__(16) float sRaw[4][16 * TR];   // per wave: long-range q.k [query][tap]
+  // Per wave: long-range q.k [query][tap].  With scale_embed the scores are added into the T table
+  // instead (its long-range entries are read once, after every tap is scored).
+  __shared__ __align__(16) float sRaw[HAS_SE ? 1 : 4][HAS_SE ? 4 : 16 * TR];
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
 
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC
   // Long-range q.k on the VALU: each lane dots its 16-byte chunk, the CPR lanes of a row sum
   // (DPP), and one lane per row files the score in the wave's [query][tap] table.  The first
   // half's registers are free before the second half is loaded.
-  float* sRw = sRaw[w];
+  float* sRw = sRaw[HAS_SE ? 0 : w];
   // Score of long-range tap t for each of the wave's rows, less the bias and q.se term
   // (log2 units): gain c log2e q.k, one DPP sum per row.
   auto sparse_score = [&](int t) {
@@ -195,7 +197,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC
     for (int u = 0; u < CHW; ++u) {
       float d = sGain2[j] * dot8_bf16(qR[u], kS[t][u], 0.f);
       d = group_sum<G_::CPRP>(d);
-      if (rc_chunk<D>(l, u) == 0) sRw[rc_row<D>(l, u) * TR + t] = d;
+      if (rc_chunk<D>(l, u) == 0) {
+        if constexpr (HAS_SE) sTw[rc_row<D>(l, u) * TS + j] += d;
+        else sRw[rc_row<D>(l, u) * TR + t] = d;
+      }
     }
   };
 #pragma unroll
@@ -253,7 +258,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE || NSC
     ss[t] = -INFINITY;
     if (NSC > 0 || t < NS) {
       const int j = W + 1 + t;
-      const float v = sRw[i * TR + t] + (HAS_SE ? sTw[i * TS + j] : sBias2[j]);
+      const float v = HAS_SE ? sTw[i * TS + j] : sRw[i * TR + t] + sBias2[j];
       ss[t] = (diag && row_ok && n >= dl_s[t]) ? v : -INFINITY;
     }
   }
