@@ -194,8 +194,10 @@ def bench_decode(dev, steps=1000, layers=8):
 
 def bench_module(dev, steps=20, warmup=20):
     """DSQGAttentionQW (E768 H12, the config-2 attention layer) fwd+bwd in bf16 on x [8,2048,768]:
-    as shipped (q, k, v strided views of the qkv projection) and with the reference's
-    permute().contiguous() copies put back (train/train_2048_condU.py:173-175)."""
+    as shipped (q, k, v strided views of the qkv projection), with the reference's
+    permute().contiguous() copies put back (train/train_2048_condU.py:173-175), and with a K/V
+    injection in the path; plus the injection adds and the gate multiply timed alone (what a fold
+    of either into the kernels could save at most)."""
     import torch
     from dwarf_amd import dsqg_attention
     from dwarf_amd.modules import DSQGAttentionQW, _heads
@@ -222,6 +224,33 @@ def bench_module(dev, steps=20, warmup=20):
         ms = _events_ms(step, steps, stream)
         res[f"ms_per_step_{name}"] = round(ms, 4)
     res["tok_per_s"] = round(B * N / (res["ms_per_step_strided_views"] * 1e-3), 1)
+
+    # The two elementwise steps around the kernels that a fold into the kernels could remove
+    # (train/train_2048_condU.py:178-181, 190-191), each timed alone (fwd+bwd, same shapes), and the
+    # module with the K/V injection in its path (deltas requiring grad, as the block's are).
+    kd, vd = (torch.randn(B, H, N, E // H, device=dev, dtype=torch.bfloat16, requires_grad=True)
+              for _ in range(2))
+    qkv = torch.randn(B, N, 3 * E, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    dk_up = torch.randn(B, H, N, E // H, device=dev, dtype=torch.bfloat16)
+    o_flat = torch.randn(B, N, E, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    g_pre = torch.randn(B, N, E, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    gate = torch.sigmoid(g_pre).detach().requires_grad_(True)
+
+    def inject_step(i):
+        _, k, v = _heads(qkv, B, N, H, E // H)
+        torch.autograd.backward([k + kd, v + vd], [dk_up, dk_up])
+
+    def gate_step(i):
+        (o_flat * gate).backward(dy)
+
+    def module_inject_step(i):
+        m(x, kv_inject=(kd, vd)).backward(dy)
+
+    for name, fn in (("kv_inject_adds", inject_step), ("gate_multiply", gate_step),
+                     ("module_with_kv_inject", module_inject_step)):
+        for i in range(warmup):
+            fn(i)
+        res[f"ms_{name}"] = round(_events_ms(fn, steps, stream), 4)
     return res
 
 
@@ -601,8 +630,11 @@ def main(argv=None):
               file=sys.stderr, flush=True)
     if not args.no_module:
         result["module"] = bench_module(dev)
-        print(f"[bench] module QW fwd+bwd {result['module']['ms_per_step_strided_views']} ms "
-              f"(with permute copies {result['module']['ms_per_step_contiguous_copies']} ms)",
+        mres = result["module"]
+        print(f"[bench] module QW fwd+bwd {mres['ms_per_step_strided_views']} ms "
+              f"(with permute copies {mres['ms_per_step_contiguous_copies']} ms, with K/V "
+              f"injection {mres['ms_module_with_kv_inject']} ms; injection adds alone "
+              f"{mres['ms_kv_inject_adds']} ms, gate multiply alone {mres['ms_gate_multiply']} ms)",
               file=sys.stderr, flush=True)
     if not args.no_pool:
         result["pool"] = bench_pool(dev)

@@ -85,11 +85,14 @@ def dsqg_attention_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor,
                        scale_embed: Optional[Tensor] = None, *,
                        offsets: Optional[Sequence[int]] = None,
                        score_gain: Optional[Tensor] = None,
-                       if_gain: Optional[Tensor] = None) -> Tensor:
+                       if_gain: Optional[Tensor] = None,
+                       kv_inject=None) -> Tensor:
     """dsqg_attention on q, k, v = the head views of qkv [B,N,3*H*HD] (the qkv_proj output).
 
     Same result as ``dsqg_attention(*split_qkv(qkv, num_heads), ...)``; differentiable in qkv
-    and every parameter, with d(qkv) produced as one tensor.
+    and every parameter, with d(qkv) produced as one tensor.  ``kv_inject=(k_delta, v_delta)``
+    ([B,H,N,HD] each) attends K + k_delta and V + v_delta (the Huygens injection of
+    train/train_2048_condU.py:178-181); the deltas' gradients are the K / V slices of d(qkv).
     """
     assert qkv.dim() == 3, f"qkv must be [B,N,3*H*HD], got {tuple(qkv.shape)}"
     offs = validate(offsets) if offsets is not None else default_offsets(pos_bias.shape[0])
@@ -98,9 +101,17 @@ def dsqg_attention_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor,
     orig = qkv.dtype
     if orig not in (torch.float32, torch.bfloat16):
         qkv = qkv.bfloat16()
-    args = (qkv, num_heads, pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain),
-            list(offs))
-    out, _ = ops.dsqg_fwd_qkv(*args) if ops.traced(qkv) else ops.AttentionQkvFn.apply(*args)
+    params = (pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain), list(offs))
+    if kv_inject is None:
+        args = (qkv, num_heads, *params)
+        out, _ = ops.dsqg_fwd_qkv(*args) if ops.traced(qkv) else ops.AttentionQkvFn.apply(*args)
+    else:
+        k_delta, v_delta = kv_inject
+        assert k_delta.shape == k.shape and v_delta.shape == v.shape, \
+            f"kv_inject deltas must be {tuple(k.shape)}"
+        args = (qkv, k_delta, v_delta, num_heads, *params)
+        fn = ops.dsqg_fwd_qkv_kv if ops.traced(qkv, k_delta, v_delta) else ops.AttentionQkvKvFn.apply
+        out = fn(*args)[0]
     return out if out.dtype == orig else out.to(orig)
 
 

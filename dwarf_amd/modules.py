@@ -39,7 +39,7 @@ import torch.nn.functional as F
 from torch import Tensor, nn
 
 from . import ops
-from .api import DSQGRingCache, causal_mean_pool_gate, dsqg_attention, dsqg_attention_qkv
+from .api import DSQGRingCache, causal_mean_pool_gate, dsqg_attention_qkv
 from .offsets import OFFSETS_V3, validate
 
 
@@ -77,18 +77,14 @@ class _DSQGBase(nn.Module):
         B, N, D = x.shape
         H, HD = self.num_heads, self.head_dim
         qkv = self.qkv_proj(x)
-        if kv_inject is None:
-            out = dsqg_attention_qkv(qkv, H, self.pos_bias, scale_embed, offsets=self._offsets,
-                                     if_gain=if_gain)
-            k, v = ops.split_qkv(qkv, H)[1:]
-        else:
-            q, k, v = _heads(qkv, B, N, H, HD)
-            k_delta, v_delta = kv_inject
-            k, v = k + k_delta, v + v_delta
-            out = dsqg_attention(q, k, v, self.pos_bias, scale_embed, offsets=self._offsets,
-                                 if_gain=if_gain)
+        out = dsqg_attention_qkv(qkv, H, self.pos_bias, scale_embed, offsets=self._offsets,
+                                 if_gain=if_gain, kv_inject=kv_inject)
         if cache is not None:
-            cache.prefill(k.detach(), v.detach())
+            with torch.no_grad():
+                k, v = ops.split_qkv(qkv, H)[1:]
+                if kv_inject is not None:
+                    k, v = k + kv_inject[0], v + kv_inject[1]
+                cache.prefill(k, v)
         out_flat = out.permute(0, 2, 1, 3).reshape(B, N, D)
         gate = torch.sigmoid(self.gate_proj(x))
         return self.dropout(self.out_proj(out_flat * gate))

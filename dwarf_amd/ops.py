@@ -312,8 +312,10 @@ def dsqg_bwd_qkv(qkv: Tensor, num_heads: int, dout: Tensor, lse: Tensor, pos_bia
 
 
 def _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
-                  need_dse, need_dg, need_da):
+                  need_dse, need_dg, need_da, k_eff=None, v_eff=None):
     q, k, v = split_qkv(qkv, num_heads)
+    if k_eff is not None:  # K/V with the injection added (dsqg_fwd_qkv_kv)
+        k, v = k_eff, v_eff
     dqkv = torch.empty_like(qkv, memory_format=torch.contiguous_format)
     launch = BwdLaunch(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
                        need_dse, need_dg, need_da, grads=split_qkv(dqkv, num_heads))
@@ -337,6 +339,99 @@ def _(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, off
 
 torch.library.register_autograd("dwarf::dsqg_fwd_qkv", _backward_qkv,
                                 setup_context=_setup_context_qkv)
+
+
+# K/V injection (train/train_2048_condU.py:178-181: k + k_delta, v + v_delta before the kernel):
+# one add per operand in the forward, and a backward that writes dq, dk, dv once into d(qkv),
+# whose K and V slices are also the gradients of k_delta and v_delta (the add passes its
+# gradient to both summands), so autograd assembles nothing.
+
+def _kv_eff(qkv: Tensor, k_delta: Tensor, v_delta: Tensor, num_heads: int):
+    _, k, v = split_qkv(qkv, num_heads)
+    return k + k_delta.to(k.dtype), v + v_delta.to(v.dtype)
+
+
+@torch.library.custom_op("dwarf::dsqg_fwd_qkv_kv", mutates_args=())
+def dsqg_fwd_qkv_kv(qkv: Tensor, k_delta: Tensor, v_delta: Tensor, num_heads: int,
+                    pos_bias: Tensor, scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
+                    if_gain: Optional[Tensor],
+                    offsets: List[int]) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(out, lse, k + k_delta, v + v_delta): dsqg_fwd on q = the query view of qkv and the
+    injected K/V (returned for the backward)."""
+    k_eff, v_eff = _kv_eff(qkv, k_delta, v_delta, num_heads)
+    q = split_qkv(qkv, num_heads)[0]
+    launch = FwdLaunch(q, k_eff, v_eff, pos_bias, scale_embed, score_gain, if_gain, offsets)
+    launch.run()
+    return launch.out, launch.lse, k_eff, v_eff
+
+
+@dsqg_fwd_qkv_kv.register_fake
+def _(qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets):
+    B, N, E3 = qkv.shape
+    HD = E3 // (3 * num_heads)
+    return (qkv.new_empty((B, N, num_heads, HD)).permute(0, 2, 1, 3),
+            qkv.new_empty((B, num_heads, N), dtype=torch.float32),
+            qkv.new_empty((B, num_heads, N, HD)), qkv.new_empty((B, num_heads, N, HD)))
+
+
+@torch.library.custom_op("dwarf::dsqg_bwd_qkv_kv", mutates_args=())
+def dsqg_bwd_qkv_kv(qkv: Tensor, k_eff: Tensor, v_eff: Tensor, num_heads: int, dout: Tensor,
+                    lse: Tensor, pos_bias: Tensor, scale_embed: Optional[Tensor],
+                    score_gain: Optional[Tensor], if_gain: Optional[Tensor], offsets: List[int],
+                    need_dse: bool, need_dg: bool,
+                    need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """dsqg_bwd_qkv with the injected K/V: (dqkv, dpos_bias, dscale_embed, dscore_gain, dif_gain)."""
+    return _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain,
+                         offsets, need_dse, need_dg, need_da, k_eff, v_eff)
+
+
+@dsqg_bwd_qkv_kv.register_fake
+def _(qkv, k_eff, v_eff, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain,
+      offsets, need_dse, need_dg, need_da):
+    B, N, E3 = qkv.shape
+    HD = E3 // (3 * num_heads)
+    J = len(offsets)
+    f = dict(dtype=torch.float32)
+    return (qkv.new_empty(qkv.shape), qkv.new_empty((J, num_heads), **f),
+            qkv.new_empty((J, HD) if need_dse else (0,), **f),
+            qkv.new_empty((num_heads, J) if need_dg else (0,), **f),
+            qkv.new_empty((num_heads,) if need_da else (0,), **f))
+
+
+def _setup_context_qkv_kv(ctx, inputs, output):
+    qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets = inputs
+    _, lse, k_eff, v_eff = output
+    ctx.save_for_backward(qkv, k_eff, v_eff, lse, pos_bias, scale_embed, score_gain, if_gain)
+    ctx.num_heads = num_heads
+    ctx.offsets = list(offsets)
+    ctx.delta_dtypes = (k_delta.dtype, v_delta.dtype)
+    ctx.mark_non_differentiable(lse, k_eff, v_eff)
+
+
+def _backward_qkv_kv(ctx, dout, _dlse, _dk_eff, _dv_eff, direct: bool = False):
+    qkv, k_eff, v_eff, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    need_dse = bool(need[5]) and scale_embed is not None
+    need_dg = bool(need[6]) and score_gain is not None
+    need_da = bool(need[7]) and if_gain is not None
+    args = (qkv, k_eff, v_eff, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias, scale_embed,
+            score_gain, if_gain, ctx.offsets, need_dse, need_dg, need_da)
+    if direct:
+        dqkv, dpb, dse, dg, da = _bwd_qkv_impl(
+            qkv, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias, scale_embed, score_gain,
+            if_gain, ctx.offsets, need_dse, need_dg, need_da, k_eff, v_eff)
+    else:
+        dqkv, dpb, dse, dg, da = dsqg_bwd_qkv_kv(*args)
+    _, dk, dv = split_qkv(dqkv, ctx.num_heads)
+    return (dqkv, dk.to(ctx.delta_dtypes[0]), dv.to(ctx.delta_dtypes[1]), None,
+            dpb.to(pos_bias.dtype),
+            dse.to(scale_embed.dtype) if need_dse else None,
+            dg.to(score_gain.dtype) if need_dg else None,
+            da.to(if_gain.dtype) if need_da else None, None)
+
+
+torch.library.register_autograd("dwarf::dsqg_fwd_qkv_kv", _backward_qkv_kv,
+                                setup_context=_setup_context_qkv_kv)
 
 
 # Eager autograd over the same launch objects: the custom ops above are what traced code
@@ -381,6 +476,24 @@ class AttentionQkvFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, dlse):
         return _backward_qkv(ctx, dout, dlse, direct=True)
+
+
+class AttentionQkvKvFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed, score_gain, if_gain,
+                offsets):
+        k_eff, v_eff = _kv_eff(qkv, k_delta, v_delta, num_heads)
+        q = split_qkv(qkv, num_heads)[0]
+        launch = FwdLaunch(q, k_eff, v_eff, pos_bias, scale_embed, score_gain, if_gain, offsets)
+        launch.run()
+        _setup_context_qkv_kv(ctx, (qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed,
+                                    score_gain, if_gain, offsets),
+                              (launch.out, launch.lse, k_eff, v_eff))
+        return launch.out, launch.lse, k_eff, v_eff
+
+    @staticmethod
+    def backward(ctx, dout, dlse, dk_eff, dv_eff):
+        return _backward_qkv_kv(ctx, dout, dlse, dk_eff, dv_eff, direct=True)
 
 
 # ------------------------------------------------------------------------------------------

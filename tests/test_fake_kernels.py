@@ -40,6 +40,14 @@ def test_forward_and_backward_ops(fake):
     dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv(qkv, H, q, lse, pb, None, None, None,
                                               list(OFFSETS_V3), True, True, False)
     assert dqkv.shape == qkv.shape and dse.shape == (J, D) and dg.shape == (H, J)
+    # K/V injection: the injected K/V come back for the backward, which returns one d(qkv).
+    out, lse, k_eff, v_eff = ops.dsqg_fwd_qkv_kv(qkv, q, q, H, pb, None, None, None,
+                                                 list(OFFSETS_V3))
+    assert out.shape == (B, H, N, D) and lse.shape == (B, H, N)
+    assert k_eff.shape == (B, H, N, D) and v_eff.shape == (B, H, N, D)
+    dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv_kv(qkv, k_eff, v_eff, H, q, lse, pb, None, None,
+                                                 None, list(OFFSETS_V3), False, False, False)
+    assert dqkv.shape == qkv.shape and dpb.shape == (J, H) and dse.numel() == 0
 
 
 def test_decode_and_pool_ops(fake):

@@ -129,19 +129,44 @@ def test_module_forward_backward_matches_oracle(gpu_device, cls, dtype):
 
 
 @pytest.mark.gpu
-def test_module_kv_inject(gpu_device):
-    """Huygens K/V injection: k + k_delta, v + v_delta, q unchanged."""
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_module_kv_inject(gpu_device, dtype):
+    """Huygens K/V injection (k + k_delta, v + v_delta, q unchanged): output and the gradients
+    of x, both deltas and every parameter against the reference forward through the oracle.
+    The deltas' gradients come back as the K / V slices of d(qkv).  Tolerance as in
+    test_module_forward_backward_matches_oracle."""
     torch.manual_seed(12)
-    E, H, B, N = 256, 4, 1, 200
+    E, H, B, N = 256, 4, 2, 300
     m = DSQGAttentionQW(E, H, dropout=0.0)
-    x = torch.randn(B, N, E)
-    kd = 0.5 * torch.randn(B, H, N, E // H)
-    vd = 0.5 * torch.randn(B, H, N, E // H)
-    ref, _ = _reference_forward(m, x, (kd, vd))
-    mg = m.to(gpu_device)
-    y = mg(x.to(gpu_device), kv_inject=(kd.to(gpu_device), vd.to(gpu_device)))
-    err = (y.detach().cpu() - ref.detach()).abs().max().item()
-    assert err <= 1e-4 * ref.abs().max().item()
+    with torch.no_grad():
+        m.pos_bias.add_(0.3 * torch.randn_like(m.pos_bias))
+        m.scale_embed.copy_(0.5 * torch.randn_like(m.scale_embed))
+        m.if_gain.copy_(0.8 + 0.4 * torch.rand_like(m.if_gain))
+    x = torch.randn(B, N, E).to(dtype).float().requires_grad_(True)
+    kd = (0.5 * torch.randn(B, H, N, E // H)).to(dtype).float().requires_grad_(True)
+    vd = (0.5 * torch.randn(B, H, N, E // H)).to(dtype).float().requires_grad_(True)
+    dy = torch.randn(B, N, E).to(dtype).float()
+    ref, p = _reference_forward(m, x, (kd, vd))
+    ref.backward(dy)
+
+    mg = m.to(gpu_device, dtype)
+    xg, kdg, vdg = (t.detach().to(gpu_device, dtype).requires_grad_(True) for t in (x, kd, vd))
+    y = mg(xg, kv_inject=(kdg, vdg))
+    y.backward(dy.to(gpu_device, dtype))
+    tol = 1e-4 if dtype == torch.float32 else 3e-2
+
+    def close(a, b, what):
+        a = a.float().cpu()
+        scale = max(1.0, b.abs().max().item()) if dtype == torch.bfloat16 else b.abs().max().item()
+        err = (a - b).abs().max().item()
+        assert err <= tol * scale, f"kv_inject {dtype} {what}: max err {err:.3g} vs scale {scale:.3g}"
+
+    close(y.detach(), ref.detach(), "output")
+    close(xg.grad, x.grad, "grad x")
+    close(kdg.grad, kd.grad, "grad k_delta")
+    close(vdg.grad, vd.grad, "grad v_delta")
+    for name, prm in mg.named_parameters():
+        close(prm.grad, p[name].grad, f"grad {name}")
 
 
 @pytest.mark.gpu
