@@ -323,13 +323,28 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     }
   }
 
-  if (key_ok) {
-    bf16_t* dkr = static_cast<bf16_t*>(p.dk) + b * p.dks.b + h * p.dks.h + m * p.dks.n + 4 * g;
-    bf16_t* dvr = static_cast<bf16_t*>(p.dv) + b * p.dvs.b + h * p.dvs.h + m * p.dvs.n + 4 * g;
+  // dk, dv (MFMA layout: lane (i, g) holds key i, d = 16 db + 4 g + 0..3) leave as whole rows
+  // through the wave's staging rows of the window tiles (free after the last tap), then 16-byte
+  // row pieces per lane.
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last tap's transposed reads are done
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      *reinterpret_cast<uint2*>(dkr + 16 * db) = pack_bf16x4_u2(dK[db][0], dK[db][1], dK[db][2], dK[db][3]);
-      *reinterpret_cast<uint2*>(dvr + 16 * db) = pack_bf16x4_u2(dV[db][0], dV[db][1], dV[db][2], dV[db][3]);
+  for (int db = 0; db < DB; ++db) {
+    *reinterpret_cast<uint2*>(qsw + i * RV + 16 * db + 4 * g) = pack_bf16x4_u2(dK[db][0], dK[db][1], dK[db][2], dK[db][3]);
+    *reinterpret_cast<uint2*>(osw + i * RV + 16 * db + 4 * g) = pack_bf16x4_u2(dV[db][0], dV[db][1], dV[db][2], dV[db][3]);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
+  __builtin_amdgcn_wave_barrier();
+  {
+    bf16_t* dkb = static_cast<bf16_t*>(p.dk) + b * p.dks.b + h * p.dks.h;
+    bf16_t* dvb = static_cast<bf16_t*>(p.dv) + b * p.dvs.b + h * p.dvs.h;
+#pragma unroll
+    for (int u = 0; u < CHW; ++u) {
+      const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+      if (m0w + rr < N && cc < CPR) {
+        st16(dkb + (m0w + rr) * p.dks.n + 8 * cc, *reinterpret_cast<const uint4*>(qsw + rr * RV + 8 * cc));
+        st16(dvb + (m0w + rr) * p.dvs.n + 8 * cc, *reinterpret_cast<const uint4*>(osw + rr * RV + 8 * cc));
+      }
     }
   }
 }

@@ -428,14 +428,33 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
         }
       }
     }
-    if (row_ok) {
+    // dq (MFMA layout: lane (i, g) holds query i, d = 16 db + 4 g + 0..3) leaves as whole rows
+    // through a wave-private LDS block (the K staging block; with scale_embed it holds the Q
+    // rows for dse, and the wave's rows of the K window, free since the barrier after the band,
+    // take its place), then 16-byte row pieces per lane.  Without a free block (scale_embed at
+    // D = 32, whose tables stay outside the V window) the quads are stored directly.
+    if constexpr (!HAS_SE || TBL_IN_V) {
+      bf16_t* const stg = HAS_SE ? sK + 16 * w * RV : sKsw;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+        *reinterpret_cast<uint2*>(stg + i * RV + 16 * db + 4 * g) =
+            pack_bf16x4_u2(c * dQ[db][0], c * dQ[db][1], c * dQ[db][2], c * dQ[db][3]);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+        if (n0w + rr < N && cc < CPR)
+          st16(dqb + (n0w + rr) * p.dqs.n + 8 * cc, *reinterpret_cast<const uint4*>(stg + rr * RV + 8 * cc));
+      }
+    } else if (row_ok) {
       bf16_t* o = dqb + n * p.dqs.n + 4 * g;
 #pragma unroll
       for (int db = 0; db < DB; ++db)
         *reinterpret_cast<uint2*>(o + 16 * db) =
             pack_bf16x4_u2(c * dQ[db][0], c * dQ[db][1], c * dQ[db][2], c * dQ[db][3]);
-      if (g == 0) p.dpre[rowbase + n] = Dp;
     }
+    if (row_ok && g == 0) p.dpre[rowbase + n] = Dp;
 
     // dbias / dg column sums of this wave's 16 table rows (its own writes, complete above),
     // and the wave's sum of D' (for da): no workgroup barrier inside the tile.
