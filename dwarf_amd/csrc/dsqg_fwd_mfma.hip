@@ -100,11 +100,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
     wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
   }
+  // The band's B operand (query rows in the MFMA operand order).  With scale_embed it is loaded
+  // from global memory here (the T table needs it first); without, it is read after the window
+  // barrier from the whole-row copy below, staged in the wave's block (free until the
+  // long-range P V), which saves the operand-order global loads (16 rows x 16 B per 16 lanes).
   const int qlane = opaque(i * qsn + 8 * g);
   bf16x8_t qB[KS];
+  if constexpr (HAS_SE) {
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
-    qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (8 * g + 32 * s < D ? qlane + 32 * s : kNoElem)));
+    for (int s = 0; s < KS; ++s)
+      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (8 * g + 32 * s < D ? qlane + 32 * s : kNoElem)));
+  }
   // The same query rows and the long-range key rows n0w - delta + 0..15 in the row-chunk
   // layout (whole rows per 8 lanes); the keys in two halves (the second after the dense band has
   // consumed its registers) to bound the register peak.
@@ -172,7 +178,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
       st16(sK + r * RV + cc * 8, wk[u]);
     }
   }
+  if constexpr (!HAS_SE) {
+#pragma unroll
+    for (int u = 0; u < CHW; ++u)
+      if (rc_valid<D>(l, u)) st16(sVs[w] + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
+  }
   __syncthreads();
+  if constexpr (!HAS_SE) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qB[s] = 8 * g + 32 * s < D ? as_bf16x8(*reinterpret_cast<const uint4*>(sVs[w] + i * RV + 8 * g + 32 * s))
+                                 : as_bf16x8(zero16());
+  }
 
   // ---- Dense band scores: S^T = K_band Q^T. ----
   f32x4_t accS[3];
