@@ -35,7 +35,9 @@ namespace dsqg {
 // Row stride of the per-wave [query][tap] tables (floats; 16 B aligned rows, 48 taps).
 constexpr int kDqTableStride = 48;
 
-template <int D, bool HAS_SE, int NSC>
+// DG: the score gain's gradient is requested (its c q.k table in dynamic LDS and the extra row
+// sums are compiled in only then).
+template <int D, bool HAS_SE, int NSC, bool DG>
 __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC != 11) ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
   using G_ = Geo<D>;
   constexpr int QT = 64;
@@ -90,7 +92,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   const int NS = NSC > 0 ? NSC : J - W - 1;
   const float c = p.scale, c2 = p.scale * kLog2e;
   const float a = p.if_gain ? p.if_gain[h] : 1.0f;
-  const bool se_grad = p.part_se != nullptr, g_grad = p.part_gain != nullptr;
+  const bool se_grad = p.part_se != nullptr;
+  constexpr bool g_grad = DG;
   const int qsn = (int)p.qs.n, ksn = (int)p.ks.n, vsn = (int)p.vs.n, dosn = (int)p.dos.n;
 
   const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
@@ -544,12 +547,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
 
 template <int D, bool HAS_SE>
 static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
-  const size_t dyn = p.part_gain ? sizeof(float) * 4 * 16 * kDqTableStride : 0;  // dg table
+  if (p.part_gain) {  // the score gain's gradient: the generic-table form with its dg table
+    const size_t dyn = sizeof(float) * 4 * 16 * kDqTableStride;
+    hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0, true>), dim3(nb), dim3(kBlock), dyn, st, p);
+    return;
+  }
   switch (p.taps.J - p.taps.W - 1) {
-    case 11: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 11>), dim3(nb), dim3(kBlock), dyn, st, p); break;
-    case 13: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 13>), dim3(nb), dim3(kBlock), dyn, st, p); break;
-    case 14: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 14>), dim3(nb), dim3(kBlock), dyn, st, p); break;
-    default: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+    case 11: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 11, false>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 13: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 13, false>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    case 14: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 14, false>), dim3(nb), dim3(kBlock), 0, st, p); break;
+    default: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0, false>), dim3(nb), dim3(kBlock), 0, st, p); break;
   }
 }
 
