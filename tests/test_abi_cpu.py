@@ -38,6 +38,24 @@ def test_exports_every_declared_symbol(lib):
     assert lib.dsqg_abi_version() == _lib.ABI_VERSION
 
 
+def test_probe_library_is_separate_and_rejects_bad_arguments(lib):
+    """bench.py's memory-system probes live in a library of their own (not in the product), load
+    without a GPU and refuse arguments outside their documented ranges before any launch."""
+    from dwarf_amd.build import PROBE_LIB_PATH, build_probes
+    if not PROBE_LIB_PATH.exists():
+        build_probes(verbose=False)
+    probes = ctypes.CDLL(str(PROBE_LIB_PATH))
+    vp, i64, ci = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int
+    probes.dsqg_probe_gather.argtypes = [vp, i64, ci, ci, ci, vp, vp]
+    probes.dsqg_probe_fwd_skeleton.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp]
+    fake = ctypes.c_void_p(0x1000)
+    assert probes.dsqg_probe_gather(fake, 3000, 4, 8, 16, fake, None) == -1      # not 2 KB blocks
+    assert probes.dsqg_probe_gather(fake, 1 << 21, 3, 8, 16, fake, None) == -1   # pf not 1/2/4/8
+    assert probes.dsqg_probe_gather(None, 1 << 21, 4, 8, 16, fake, None) == -1
+    assert probes.dsqg_probe_fwd_skeleton(fake, fake, fake, fake, 4, 100, 3, None) == -1  # N % 64
+    assert not hasattr(lib, "dsqg_probe_gather")
+
+
 def test_ctypes_layout_matches_c(tmp_path):
     from dwarf_amd import _lib
     probes = {
