@@ -104,3 +104,36 @@ def test_compiled_graph_matches_eager(gpu_device):
     compiled = run(torch.compile(fn, backend="aot_eager", fullgraph=True))
     for a, b in zip(eager, compiled):
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+def test_compiled_qkv_with_kv_inject_matches_eager(gpu_device):
+    """The qkv entry with a K/V injection (custom ops dsqg_fwd_qkv_kv / dsqg_bwd_qkv_kv under
+    torch.compile, aot_eager) gives the eager results bit for bit, and its gradients are those
+    of the split-head form with the adds written out."""
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(B, N, 3 * H * D, generator=g).to(gpu_device, torch.bfloat16)
+    kd, vd = (torch.randn(B, H, N, D, generator=g).to(gpu_device, torch.bfloat16) for _ in range(2))
+    pb = torch.randn(J, H, generator=g).to(gpu_device)
+    se = (0.05 * torch.randn(J, D, generator=g)).to(gpu_device)
+
+    def fn(qkv, kd, vd, pb, se):
+        out = dwarf_amd.dsqg_attention_qkv(qkv, H, pb, se, kv_inject=(kd, vd))
+        return out.float().square().sum()
+
+    def split(qkv, kd, vd, pb, se):
+        q, k, v = ops.split_qkv(qkv, H)
+        return dwarf_amd.dsqg_attention(q, k + kd, v + vd, pb, se).float().square().sum()
+
+    def run(f):
+        ins = [t.clone().requires_grad_(True) for t in (qkv, kd, vd, pb, se)]
+        loss = f(*ins)
+        loss.backward()
+        return [loss.detach()] + [t.grad for t in ins]
+
+    eager = run(fn)
+    compiled = run(torch.compile(fn, backend="aot_eager", fullgraph=True))
+    for a, b in zip(eager, compiled):
+        assert torch.equal(a, b)
+    for a, b in zip(eager, run(split)):  # same kernels on the same (bf16-rounded) K/V
+        assert torch.equal(a, b)
