@@ -80,9 +80,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   float* const sRAW = sDyn;
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain[kMaxTaps];
-  // Per wave, one long-range tap's row results: (q.k, dOut.v), or with scale_embed
-  // (score less bias, dOut.v, q.k, -).
-  __shared__ __align__(16) float sPair[4][16][HAS_SE ? 4 : 2];
+  // Per wave, one long-range tap's row results (q.k, dOut.v).
+  __shared__ __align__(16) float sPair[4][16][2];
 
   const int tid = threadIdx.x;
   const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
@@ -270,6 +269,32 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     }
     const float wsum = col_sum(wlane);
     const float D0 = wsum > 0.f ? col_sum(dlane) / wsum : 0.f;
+    if constexpr (TBL_IN_V) {
+      __syncthreads();  // every wave's band reads of sV are done: the dS tables move in
+      for (int e = l; e < 16 * (48 - J); e += 64) sDSw[(e / (48 - J)) * TS + J + e % (48 - J)] = 0.f;
+    }
+    if constexpr (HAS_SE) {
+      // T for the long-range taps (log2e (bias_j + c q.se_j), the same MFMA as the dense taps'
+      // table) waits in the taps' dS table slots until the diagonal lane reads it in the taps
+      // loop; dS overwrites it after the loop.
+#pragma unroll
+      for (int jb = 0; jb < 3; ++jb) {
+        if (16 * jb + 15 <= W) continue;
+        f32x4_t acc = zero4();
+        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+        const bf16_t* srl = sSElo + (16 * jb + i) * RV + 8 * g;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
+          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(srl + 32 * s)), qB[s], acc);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * jb + 4 * g + r;
+          if (j > W && j < J) sDSw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+        }
+      }
+    }
     f32x4_t X[DB], Y[DB];
 #pragma unroll
     for (int db = 0; db < DB; ++db) { X[db] = zero4(); Y[db] = zero4(); }
@@ -298,10 +323,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
       }
     }
 
-    if constexpr (TBL_IN_V) {
-      __syncthreads();  // every wave's band reads of sV are done: the dS tables move in
-      for (int e = l; e < 16 * (48 - J); e += 64) sDSw[(e / (48 - J)) * TS + J + e % (48 - J)] = 0.f;
-    }
     // ---- Long-range taps (diagonal of one 16x16 tile each). ----
     const bool diag = g == (i >> 2);
     const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
@@ -313,29 +334,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
         const int j = W + 1 + t;
         // q.k and dOut.v on the VALU: each lane dots its 16-byte chunk, the row's lanes sum
         // (DPP), and one lane per row hands the results to the diagonal lane through LDS.  The
-        // key rows are staged (natural row order) for the transposing reads of X and Y.  With
-        // scale_embed the score (gain c log2e q.k + c log2e q.se_j) is summed as one, and q.k
-        // only for dg.
+        // key rows are staged (natural row order) for the transposing reads of X and Y.
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
-          const float qk = dot8_bf16(qR[u], kS[t % PF][u], 0.f);
+          const float qk = group_sum<CPRP>(dot8_bf16(qR[u], kS[t % PF][u], 0.f));
           const float dv = group_sum<CPRP>(dot8_bf16(oR[u], vS[t % PF][u], 0.f));
           if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
-          if constexpr (HAS_SE) {
-            // Lanes past the row read chunk 0 (finite) against their zero query chunk.
-            const int sc8 = rc_valid<D>(l, u) ? rc_chunk<D>(l, u) * 8 : 0;
-            const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + sc8);
-            const uint4 sel = *reinterpret_cast<const uint4*>(sSElo + j * RV + sc8);
-            const float qse = dot8_bf16(qR[u], sel, dot8_bf16(qR[u], se, 0.f));
-            const float sc = group_sum<CPRP>(fmaf(c2, qse, sGain[j] * c2 * qk));
-            const float raw = g_grad ? group_sum<CPRP>(qk) : 0.f;
-            if (rc_chunk<D>(l, u) == 0)
-              *reinterpret_cast<float4*>(sPair[w][rc_row<D>(l, u)]) = float4{sc, dv, raw, 0.f};
-          } else {
-            const float dk = group_sum<CPRP>(qk);
-            if (rc_chunk<D>(l, u) == 0)
-              *reinterpret_cast<float2*>(sPair[w][rc_row<D>(l, u)]) = float2{dk, dv};
-          }
+          if (rc_chunk<D>(l, u) == 0)
+            *reinterpret_cast<float2*>(sPair[w][rc_row<D>(l, u)]) = float2{qk, dv};
         }
         if (t + PF < NS) {
           const int m0 = n0w - dl_s[t + PF];
@@ -347,14 +353,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and pairs are written
         __builtin_amdgcn_wave_barrier();
-        float raw, uval, s2;
-        if constexpr (HAS_SE) {
-          const float4 pr = *reinterpret_cast<const float4*>(sPair[w][i]);
-          raw = pr.z; uval = pr.y; s2 = pr.x + sBias2[j];
-        } else {
-          const float2 pr = *reinterpret_cast<const float2*>(sPair[w][i]);
-          raw = pr.x; uval = pr.y; s2 = fmaf(sGain[j] * c2, raw, sBias2[j]);
-        }
+        const float2 pr = *reinterpret_cast<const float2*>(sPair[w][i]);
+        const float raw = pr.x, uval = pr.y;
+        const float s2 = fmaf(sGain[j] * c2, raw, HAS_SE ? sDSw[i * TS + j] : sBias2[j]);
         const bool ok = diag && row_ok && n >= dl_s[t];
         const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
         als[t] = alpha;
