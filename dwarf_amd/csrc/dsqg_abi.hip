@@ -100,6 +100,7 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   if ((st = check_tensor(a->dv, a->dv_stride, s.dtype, ne))) return st;
   if (ne > 0 && !a->lse) return DSQG_EINVAL;
   if ((long long)s.J * s.H > 0 && (!a->pos_bias || !a->dpos_bias)) return DSQG_EINVAL;
+  if (!aligned16(a->scale_embed)) return DSQG_EINVAL;  // read as 16-byte pieces
   p->B = s.B; p->H = s.H; p->N = s.N;
   p->qs = to_strides(a->q_stride); p->ks = to_strides(a->k_stride);
   p->vs = to_strides(a->v_stride); p->dos = to_strides(a->dout_stride);
@@ -152,6 +153,7 @@ int dsqg_fwd(const dsqg_fwd_args* a, dsqg_stream_t stream) {
   if ((st = check_tensor(a->v, a->v_stride, s.dtype, ne))) return st;
   if ((st = check_tensor(a->out, a->out_stride, s.dtype, ne))) return st;
   if ((long long)s.J * s.H > 0 && !a->pos_bias) return DSQG_EINVAL;
+  if (!aligned16(a->scale_embed)) return DSQG_EINVAL;  // read as 16-byte pieces
   if ((long long)s.B * s.H * ((s.N + 15) / 16) > INT_MAX / 2) return DSQG_EINVAL;
   if (ne == 0) return DSQG_OK;
   p.B = s.B; p.H = s.H; p.N = s.N;

@@ -105,7 +105,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
   }
 
-  // ---- Loads. ----
+  // ---- Loads (scale_embed first: the T table waits for it alone). ----
+  SeRows<D> seR;
+  if constexpr (HAS_SE) seR.load(p.scale_embed, J, tid);
   uint4 wq[CWIN], wo[CWIN];
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
@@ -153,14 +155,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     sGain2[j] = gj * c2;
     sGainC[j] = gj * c;
   }
-  if constexpr (HAS_SE) {
-    constexpr int DP = G_::DP;
-    for (int e = tid; e < SEJ * DP; e += kBlock) {
-      const int j = e / DP, d = e - j * DP;
-      const float x = j < J && d < D ? p.scale_embed[j * D + d] : 0.f;
-      sSE[j * RV + d] = __builtin_bit_cast(bf16_t, (__bf16)x);
-    }
-  }
+  if constexpr (HAS_SE) seR.template store<RV>(sSE, nullptr, tid);
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;

@@ -120,12 +120,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     sGain[j] = gj;
   }
   if constexpr (HAS_SE) {
-    constexpr int DP = G_::DP;
-    for (int e = tid; e < SEJ * DP; e += kBlock) {
-      const int j = e / DP, d = e - j * DP;
-      split_bf16(j < J && d < D && p.scale_embed ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d],
-                 sSElo[j * RV + d]);
-    }
+    SeRows<D> seR;
+    seR.load(p.scale_embed, J, tid);
+    seR.template store<RV>(sSE, sSElo, tid);
   }
 
   float* const sDS = TBL_IN_V ? reinterpret_cast<float*>(sV) : sDSst;

@@ -91,6 +91,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   load_sparse_deltas(p.taps, dl_s);
 
   // ---- Global loads (all zero-filled outside [0, N) by the buffer range check). ----
+  // scale_embed and the band's query operand go first: the T table waits for them alone.
+  SeRows<D> seR;
+  if constexpr (HAS_SE) seR.load(p.scale_embed, J, tid);
+  const int qlane = opaque(i * qsn + 8 * g);
+  bf16x8_t qB[KS];
+  if constexpr (HAS_SE) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (8 * g + 32 * s < D ? qlane + 32 * s : kNoElem)));
+  }
   // Offsets are (uniform row) * stride + (per-lane part), so the row products stay scalar.
   uint4 wv[CWIN], wk[CWIN];
 #pragma unroll
@@ -100,17 +110,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
     wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
   }
-  // The band's B operand (query rows in the MFMA operand order).  With scale_embed it is loaded
-  // from global memory here (the T table needs it first); without, it is read after the window
-  // barrier from the whole-row copy below, staged in the wave's block (free until the
-  // long-range P V), which saves the operand-order global loads (16 rows x 16 B per 16 lanes).
-  const int qlane = opaque(i * qsn + 8 * g);
-  bf16x8_t qB[KS];
-  if constexpr (HAS_SE) {
-#pragma unroll
-    for (int s = 0; s < KS; ++s)
-      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (8 * g + 32 * s < D ? qlane + 32 * s : kNoElem)));
-  }
+  // The band's B operand (query rows in the MFMA operand order): with scale_embed loaded from
+  // global memory above (the T table needs it first); without, read after the window barrier
+  // from the whole-row copy below, staged in the wave's block (free until the long-range P V),
+  // which saves the operand-order global loads (16 rows x 16 B per 16 lanes).
   // The same query rows and the long-range key rows n0w - delta + 0..15 in the row-chunk
   // layout (whole rows per 8 lanes); the keys in two halves (the second after the dense band has
   // consumed its registers) to bound the register peak.
@@ -145,11 +148,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     // fp32 precision to about 2^-17.
     bf16_t* const sSE = sK;
     bf16_t* const sSElo = sV;
-    constexpr int DP = G_::DP;
-    for (int e = tid; e < 48 * DP; e += kBlock) {
-      const int j = e / DP, d = e - j * DP;
-      split_bf16(j < J && d < D ? p.scale_embed[j * D + d] : 0.f, sSE[j * RV + d], sSElo[j * RV + d]);
-    }
+    seR.template store<RV>(sSE, sSElo, tid);
     __syncthreads();
 #pragma unroll
     for (int jb = 0; jb < 3; ++jb) {

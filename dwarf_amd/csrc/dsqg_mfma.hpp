@@ -200,6 +200,43 @@ __device__ __forceinline__ void split_bf16(float x, bf16_t& hi, bf16_t& lo) {
   lo = __builtin_bit_cast(bf16_t, (__bf16)(x - (float)hb));
 }
 
+// scale_embed [J, D] (fp32, 16-byte aligned) as 48 rows x DP bf16 in LDS (row stride RV; rows
+// >= J and columns >= D zero), optionally with a second plane lo = bf16(se - hi).  The rows come
+// in as 16-byte pieces, loaded into registers first (load) and staged later (store), so a kernel
+// can issue these loads ahead of its bulk loads and wait for them alone.
+template <int D>
+struct SeRows {
+  static constexpr int C4 = Geo<D>::DP / 4;  // 4-float pieces per staged row
+  static constexpr int U = (48 * C4 + kBlock - 1) / kBlock;
+  float4 x[U];
+  __device__ __forceinline__ void load(const float* se, int J, int tid) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = tid + u * kBlock, j = e / C4, d = 4 * (e - j * C4);
+      x[u] = se && e < 48 * C4 && j < J && d < D ? *reinterpret_cast<const float4*>(se + j * D + d)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  template <int RV>
+  __device__ __forceinline__ void store(bf16_t* hi, bf16_t* lo, int tid) const {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = tid + u * kBlock, j = e / C4, d = 4 * (e - j * C4);
+      if (e < 48 * C4) {
+        const float v[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
+        bf16_t h[4], o[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) split_bf16(v[k], h[k], o[k]);
+        *reinterpret_cast<uint2*>(hi + j * RV + d) =
+            make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
+        if (lo)
+          *reinterpret_cast<uint2*>(lo + j * RV + d) =
+              make_uint2(o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16));
+      }
+    }
+  }
+};
+
 // Max / sum over the four lanes {i, i+16, i+32, i+48} that share column i of an MFMA tile.
 // v_permlane16_swap / v_permlane32_swap (gfx950) hand every lane the pair {x[l], x[l^16]}
 // (resp. x[l^32]) without an LDS round trip; the pair is combined in the same order on both

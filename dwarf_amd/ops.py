@@ -54,9 +54,10 @@ def _rows_ready(t: Tensor) -> Tensor:
 
 
 def _param(t: Optional[Tensor]) -> Optional[Tensor]:
-    if t is None or (t.dtype == torch.float32 and t.is_contiguous()):
+    # fp32, contiguous and 16-byte aligned (the kernels read scale_embed as 16-byte pieces).
+    if t is None or (t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0):
         return t  # only its pointer is passed on; the launch keeps a reference
-    return t.detach().to(torch.float32).contiguous()
+    return t.detach().to(torch.float32).clone(memory_format=torch.contiguous_format)
 
 
 def _strides(t: Tensor):

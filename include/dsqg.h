@@ -21,7 +21,7 @@
  *    order [B,H,N,D]; the innermost (D) stride must be 1 and the other strides and the base
  *    pointers must keep every row 16-byte aligned.
  *  - pos_bias / scale_embed / score_gain / if_gain and the parameter gradients are fp32 and
- *    contiguous.  q/k/v/out/dout/dq/dk/dv share one element type (dtype).
+ *    contiguous; dsqg_fwd and dsqg_bwd also need scale_embed (when given) 16-byte aligned.  q/k/v/out/dout/dq/dk/dv share one element type (dtype).
  *
  * Reference interfaces replaced (paths are in the Lanerra/DWARF tree):
  *  - dsqg_fwd        <- _DSQGFnV3.forward, kernels/dsqg_attention_v3.py:361-387

@@ -136,6 +136,8 @@ def test_fwd_rejects_bad_arguments(lib):
     assert _call_fwd(lib, a) == E
     a = _fwd_args(); a.pos_bias = None
     assert _call_fwd(lib, a) == E
+    a = _fwd_args(); a.scale_embed = 0x10004
+    assert _call_fwd(lib, a) == E                      # scale_embed read as 16-byte pieces
     a = _fwd_args(); a.shape.B = -1
     assert _call_fwd(lib, a) == E
 
@@ -177,6 +179,8 @@ def test_bwd_workspace_query_and_errors(lib):
     c = _bwd_args(); c.dpos_bias = None
     assert lib.dsqg_bwd(ctypes.byref(c), None) == _lib.DSQG_EINVAL
     assert lib.dsqg_bwd_workspace_size(ctypes.byref(c), None) == _lib.DSQG_EINVAL
+    c = _bwd_args(); c.scale_embed = 0x10008             # scale_embed not 16-byte aligned
+    assert lib.dsqg_bwd_workspace_size(ctypes.byref(c), ctypes.byref(n0)) == _lib.DSQG_EINVAL
 
 
 def test_decode_rejects_bad_arguments(lib):

@@ -273,6 +273,27 @@ def test_strided_views_match_contiguous(gpu_device):
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
+def test_misaligned_scale_embed_view_matches_aligned(gpu_device):
+    """A scale_embed view 4 bytes past a 16-byte boundary is copied to aligned memory by the
+    host layer (the kernels read it as 16-byte pieces): results equal the aligned call's."""
+    inp = _rand_inputs(2, 4, 600, 64, OFFSETS_V3, torch.bfloat16, seed=13)
+    d = {k: (None if v is None else v.to(gpu_device)) for k, v in inp.items()}
+    J, D = d["scale_embed"].shape
+    buf = torch.zeros(J * D + 1, device=gpu_device)
+    se_view = buf[1:].view(J, D)
+    se_view.copy_(d["scale_embed"])
+    assert se_view.data_ptr() % 16 == 4 and se_view.is_contiguous()
+    runs = []
+    for se in (d["scale_embed"], se_view):
+        out, lse = ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], se, d["score_gain"],
+                                d["if_gain"], list(OFFSETS_V3))
+        grads = ops.dsqg_bwd(d["q"], d["k"], d["v"], d["dout"], lse, d["pos_bias"], se,
+                             d["score_gain"], d["if_gain"], list(OFFSETS_V3), True, True, True)
+        runs.append((out, lse) + tuple(grads))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
 def test_backward_is_deterministic(gpu_device):
     inp = _rand_inputs(4, 8, 2048, 64, OFFSETS_V3, torch.bfloat16, seed=9)
     a = gpu_run(inp, OFFSETS_V3, gpu_device)
