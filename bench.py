@@ -406,14 +406,17 @@ def profile_mode(args, w, dev):
     from dwarf_amd.workloads import make_inputs
     if args.profile_kernel == "decode":
         return profile_decode(args, dev)
-    inp = make_inputs(w, device="cpu", seed=w.seed)
-    d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
-    fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
-                       d["score_gain"], d["if_gain"], list(w.offsets))
-    bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
-                       d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
-                       d["scale_embed"] is not None, d["score_gain"] is not None,
-                       d["if_gain"] is not None)
+    if args.profile_se:  # the scale_embed leg's inputs (scale_embed and if_gain)
+        _, d, fl, bl = make_sets(w, dev, 1, scale_embed=True, if_gain=True)[0]
+    else:
+        inp = make_inputs(w, device="cpu", seed=w.seed)
+        d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
+        fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
+                           d["score_gain"], d["if_gain"], list(w.offsets))
+        bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
+                           d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
+                           d["scale_embed"] is not None, d["score_gain"] is not None,
+                           d["if_gain"] is not None)
     fl.run()
     bl.run()
     torch.cuda.synchronize()
@@ -613,6 +616,8 @@ def main(argv=None):
                          "plus a plain device copy of --copy-mib MiB (the scale reference for "
                          "FETCH_SIZE / WRITE_SIZE), then exit without a JSON line")
     ap.add_argument("--profile-reps", type=int, default=5)
+    ap.add_argument("--profile-se", action="store_true",
+                    help="with --profile-kernel: the scale_embed leg's inputs (scale_embed, if_gain)")
     ap.add_argument("--probes", action="store_true",
                     help="run the memory-system probes (bench_probes.hip) and exit with their JSON line")
     ap.add_argument("--copy-mib", type=int, default=256)

@@ -32,8 +32,11 @@
 
 namespace dsqg {
 
-// Row stride of the per-wave [query][tap] tables (floats; 16 B aligned rows, 48 taps).
-constexpr int kDqTableStride = 48;
+// Row stride of the per-wave [query][tap] tables (floats; 16 B aligned rows, 48 taps).  52
+// rather than 48: the column reads of the dse product (rows 4g + 0..3, column i), the diagonal
+// lanes' long-range entries (row i, one column) and the band's dS writes then fall on distinct
+// banks (or two to a bank) instead of four to a bank.
+constexpr int kDqTableStride = 52;
 
 // DG: the score gain's gradient is requested (its c q.k table in dynamic LDS and the extra row
 // sums are compiled in only then).

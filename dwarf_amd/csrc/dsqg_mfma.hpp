@@ -35,11 +35,18 @@ __device__ __forceinline__ s16x4_t lds_read_tr16(const bf16_t* p) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-// Four floats -> packed bf16 operand (round to nearest even, v_cvt_pk_bf16_f32).
+// Two floats -> one dword of two bf16 (a in the low half), round to nearest even: a vector
+// conversion, so one v_cvt_pk_bf16_f32 takes both (element-wise conversions each take one and
+// a v_perm_b32 pairs them).
+__device__ __forceinline__ unsigned cvt_pk_bf16(float a, float b) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+// Four floats -> packed bf16 operand (round to nearest even).
 __device__ __forceinline__ s16x4_t pack_bf16x4(float a, float b, float c, float d) {
-  bf16x4_t r;
-  r[0] = (__bf16)a; r[1] = (__bf16)b; r[2] = (__bf16)c; r[3] = (__bf16)d;
-  return __builtin_bit_cast(s16x4_t, r);
+  return __builtin_bit_cast(s16x4_t, make_uint2(cvt_pk_bf16(a, b), cvt_pk_bf16(c, d)));
 }
 
 __device__ __forceinline__ uint2 pack_bf16x4_u2(float a, float b, float c, float d) {
@@ -150,10 +157,12 @@ __device__ __forceinline__ s16x4_t onehot_bf16x4(float x, int e) {
 // operand to about 2^-17 relative, where hi alone would carry 2^-9.
 __device__ __forceinline__ void split_bf16x4(float a, float b, float c, float d, s16x4_t& hi,
                                              s16x4_t& lo) {
-  bf16x4_t h;
-  h[0] = (__bf16)a; h[1] = (__bf16)b; h[2] = (__bf16)c; h[3] = (__bf16)d;
-  hi = __builtin_bit_cast(s16x4_t, h);
-  lo = pack_bf16x4(a - (float)h[0], b - (float)h[1], c - (float)h[2], d - (float)h[3]);
+  const unsigned p0 = cvt_pk_bf16(a, b), p1 = cvt_pk_bf16(c, d);
+  // The hi values back in fp32: a bf16 is the upper half of its fp32 pattern.
+  const float ha = __uint_as_float(p0 << 16), hb = __uint_as_float(p0 & 0xffff0000u);
+  const float hc = __uint_as_float(p1 << 16), hd = __uint_as_float(p1 & 0xffff0000u);
+  hi = __builtin_bit_cast(s16x4_t, make_uint2(p0, p1));
+  lo = __builtin_bit_cast(s16x4_t, make_uint2(cvt_pk_bf16(a - ha, b - hb), cvt_pk_bf16(c - hc, d - hd)));
 }
 
 __device__ __forceinline__ void split_onehot_bf16x4(float x, int e, s16x4_t& hi, s16x4_t& lo) {
@@ -223,15 +232,10 @@ struct SeRows {
     for (int u = 0; u < U; ++u) {
       const int e = tid + u * kBlock, j = e / C4, d = 4 * (e - j * C4);
       if (e < 48 * C4) {
-        const float v[4] = {x[u].x, x[u].y, x[u].z, x[u].w};
-        bf16_t h[4], o[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) split_bf16(v[k], h[k], o[k]);
-        *reinterpret_cast<uint2*>(hi + j * RV + d) =
-            make_uint2(h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16));
-        if (lo)
-          *reinterpret_cast<uint2*>(lo + j * RV + d) =
-              make_uint2(o[0] | ((unsigned)o[1] << 16), o[2] | ((unsigned)o[3] << 16));
+        s16x4_t h, o;
+        split_bf16x4(x[u].x, x[u].y, x[u].z, x[u].w, h, o);
+        *reinterpret_cast<uint2*>(hi + j * RV + d) = __builtin_bit_cast(uint2, h);
+        if (lo) *reinterpret_cast<uint2*>(lo + j * RV + d) = __builtin_bit_cast(uint2, o);
       }
     }
   }
