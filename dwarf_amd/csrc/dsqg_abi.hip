@@ -62,7 +62,7 @@ struct BwdLayout {
   int se_slices, se_per;  // two-stage dscale_embed sum: slices of se_per workgroup partials
 };
 
-constexpr size_t kMaxSeSlices = 64;
+constexpr size_t kMaxSeSlices = 256;
 
 BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
   const dsqg_shape& s = a.shape;

@@ -14,22 +14,25 @@ __global__ __launch_bounds__(kBlock) void bwd_reduce_kernel(ReduceParams r) {
   reduce_params_wave(r, blockIdx.x * (kBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), threadIdx.x & 63);
 }
 
-// First stage of the dscale_embed sum: workgroup (x, y) sums, for 256 consecutive elements of
-// [J*D], the partials of workgroups [y*se_per, (y+1)*se_per) in order.  A partial row is read
-// in 1 KB runs (one float per lane, consecutive elements), not as one float per partial row
-// per lane; the final per-element sum then reads only se_slices values.
+// First stage of the dscale_embed sum: workgroup (x, y) sums, for 1024 consecutive elements of
+// [J*D] (four per thread, one 16-byte load per partial row), the partials of workgroups
+// [y*se_per, (y+1)*se_per) in order.  Each wave reads 1 KB runs; the final per-element sum then
+// reads only se_slices values.
 __global__ __launch_bounds__(kBlock) void bwd_reduce_se_stage_kernel(ReduceParams r) {
-  const long long JD = (long long)r.J * r.D;
+  const long long JD4 = (long long)r.J * r.D / 4;  // D is a multiple of 16
   const long long t = (long long)blockIdx.x * kBlock + threadIdx.x;
-  if (t >= JD) return;
+  if (t >= JD4) return;
   const long long nb = (long long)r.B * r.H * r.n_chunks;
   const long long b0 = (long long)blockIdx.y * r.se_per;
   const long long b1 = b0 + r.se_per < nb ? b0 + r.se_per : nb;
-  const float* src = r.part_se + t;
-  float acc = 0.f;
+  const float4* src = reinterpret_cast<const float4*>(r.part_se) + t;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 8
-  for (long long blk = b0; blk < b1; ++blk) acc += src[blk * JD];
-  r.se_stage[blockIdx.y * JD + t] = acc;
+  for (long long blk = b0; blk < b1; ++blk) {
+    const float4 x = src[blk * JD4];
+    acc.x += x.x; acc.y += x.y; acc.z += x.z; acc.w += x.w;
+  }
+  reinterpret_cast<float4*>(r.se_stage)[blockIdx.y * JD4 + t] = acc;
 }
 
 bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
@@ -58,8 +61,8 @@ void bwd_plan(BwdParams& p, int D, int dtype) {
 
 hipError_t launch_bwd_reduce_se_stage(const ReduceParams& r, hipStream_t st) {
   if (r.dscale_embed && r.se_slices > 0) {
-    const long long JD = (long long)r.J * r.D;
-    hipLaunchKernelGGL(bwd_reduce_se_stage_kernel, dim3((unsigned)((JD + kBlock - 1) / kBlock), (unsigned)r.se_slices),
+    const long long JD4 = (long long)r.J * r.D / 4;
+    hipLaunchKernelGGL(bwd_reduce_se_stage_kernel, dim3((unsigned)((JD4 + kBlock - 1) / kBlock), (unsigned)r.se_slices),
                        dim3(kBlock), 0, st, r);
     return hipGetLastError();
   }
