@@ -131,10 +131,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   float* const sDS = TBL_IN_V ? reinterpret_cast<float*>(sV) : sDSst;
   // Table columns J..47 are read as zeros (whole 4-wide groups feed the MFMA operands); a table
   // in the V window gets them after the band.
-  for (int e = tid; e < 4 * 16 * (48 - J); e += kBlock) {
-    const int row = e / (48 - J), j = J + e % (48 - J);
-    if (!TBL_IN_V) sDS[row * TS + j] = 0.f;
-    if (g_grad) sRAW[row * TS + j] = 0.f;
+  // Thread t clears row t % 64 from column J + t / 64 on, every fourth column.
+  for (int j = J + (tid >> 6); j < 48; j += kBlock / 64) {
+    if (!TBL_IN_V) sDS[(tid & 63) * TS + j] = 0.f;
+    if (g_grad) sRAW[(tid & 63) * TS + j] = 0.f;
   }
 
   float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     const float D0 = wsum > 0.f ? col_sum(dlane) / wsum : 0.f;
     if constexpr (TBL_IN_V) {
       __syncthreads();  // every wave's band reads of sV are done: the dS tables move in
-      for (int e = l; e < 16 * (48 - J); e += 64) sDSw[(e / (48 - J)) * TS + J + e % (48 - J)] = 0.f;
+      for (int j = J + g; j < 48; j += 4) sDSw[i * TS + j] = 0.f;
     }
     if constexpr (HAS_SE) {
       // T for the long-range taps (log2e (bias_j + c q.se_j), the same MFMA as the dense taps'
@@ -325,6 +325,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
 
     // ---- Long-range taps (diagonal of one 16x16 tile each). ----
     const bool diag = g == (i >> 2);
+    const uint2 ohm = onehot_masks(i & 3);
     const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
     float als[NSM], uus[NSM];
 #pragma unroll
@@ -365,8 +366,15 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
         const float gal = sGain[j] * alpha;
         // One-hot weights as bf16 hi + lo pairs: the products keep the weights' fp32 precision.
         s16x4_t b1, b1l, b2, b2l;
-        split_onehot_bf16x4(gal * (uval - D0), i & 3, b1, b1l);
-        split_onehot_bf16x4(gal, i & 3, b2, b2l);
+        // With scale_embed they are placed by per-lane element masks (fewer instructions; that
+        // variant then fits without spills), without by 64-bit shifts (no extra registers).
+        if constexpr (HAS_SE) {
+          split_onehot_bf16x4(gal * (uval - D0), ohm, b1, b1l);
+          split_onehot_bf16x4(gal, ohm, b2, b2l);
+        } else {
+          split_onehot_bf16x4(gal * (uval - D0), i & 3, b1, b1l);
+          split_onehot_bf16x4(gal, i & 3, b2, b2l);
+        }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           const s16x4_t at = lds_read_tr16(ksr + 16 * db);
@@ -410,18 +418,19 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
 
-    // dq = c (a (X - D' Y) + SE^T dS^T)
+    // dq = c (a (X - D' Y) + SE^T dS^T): c a X - c a (D' - D0) Y, plus SE^T (c dS)^T.
     f32x4_t dQ[DB];
+    const float ca = c * a, cad = ca * (Dp - D0);
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) dQ[db][r] = a * (X[db][r] - (Dp - D0) * Y[db][r]);
+      for (int r = 0; r < 4; ++r) dQ[db][r] = fmaf(ca, X[db][r], -cad * Y[db][r]);
     if constexpr (HAS_SE) {
 #pragma unroll
       for (int jb = 0; jb < 3; ++jb) {
         const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
         s16x4_t bs, bsl;
-        split_bf16x4(d4.x, d4.y, d4.z, d4.w, bs, bsl);
+        split_bf16x4(c * d4.x, c * d4.y, c * d4.z, c * d4.w, bs, bsl);
         const int so = (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
@@ -442,7 +451,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
 #pragma unroll
       for (int db = 0; db < DB; ++db)
         *reinterpret_cast<uint2*>(stg + i * RV + 16 * db + 4 * g) =
-            pack_bf16x4_u2(c * dQ[db][0], c * dQ[db][1], c * dQ[db][2], c * dQ[db][3]);
+            pack_bf16x4_u2(dQ[db][0], dQ[db][1], dQ[db][2], dQ[db][3]);
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -456,7 +465,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
 #pragma unroll
       for (int db = 0; db < DB; ++db)
         *reinterpret_cast<uint2*>(o + 16 * db) =
-            pack_bf16x4_u2(c * dQ[db][0], c * dQ[db][1], c * dQ[db][2], c * dQ[db][3]);
+            pack_bf16x4_u2(dQ[db][0], dQ[db][1], dQ[db][2], dQ[db][3]);
     }
     if (row_ok && g == 0) p.dpre[rowbase + n] = Dp;
 

@@ -317,6 +317,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   // diagonal lane of query i holds a weight (the others' ss[t] are exp2(-inf) = 0), at key i.
   bf16_t* const sSt = sVs[w];
   const bf16_t* const vtr = sSt + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+  const uint2 ohm = onehot_masks(i & 3);
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
       __builtin_amdgcn_wave_barrier();
       // The weight rounded to bf16, as the dense band's P V rounds its weights.
-      const s16x4_t pb = onehot_bf16x4(ss[t] * inv, i & 3);
+      const s16x4_t pb = onehot_bf16x4(ss[t] * inv, ohm);
 #pragma unroll
       for (int db = 0; db < DB; ++db) accO[db] = mfma_16x16x16(lds_read_tr16(vtr + 16 * db), pb, accO[db]);
       __builtin_amdgcn_sched_barrier(0);

@@ -145,11 +145,18 @@ __device__ __forceinline__ void load_sparse_deltas(const TapTable& taps, int (&s
   }
 }
 
-// bf16 operand that holds x in element e (0..3) and zeros elsewhere.
-__device__ __forceinline__ s16x4_t onehot_bf16x4(float x, int e) {
-  const __bf16 hb = (__bf16)x;
-  const unsigned long long v = (unsigned long long)__builtin_bit_cast(unsigned short, hb) << (16 * e);
-  return __builtin_bit_cast(s16x4_t, v);
+// Per-lane masks that keep element e (0..3) of a 4 x bf16 operand (two dwords): the element's
+// half of dword e / 2, nothing of the other dword.  A lane's e is fixed, so the masks are made
+// once and each one-hot operand below costs two ANDs.
+__device__ __forceinline__ uint2 onehot_masks(int e) {
+  const unsigned h = (e & 1) ? 0xffff0000u : 0x0000ffffu;
+  return make_uint2(e < 2 ? h : 0u, e < 2 ? 0u : h);
+}
+
+// bf16 operand that holds x in element e (masks of onehot_masks(e)) and zeros elsewhere.
+__device__ __forceinline__ s16x4_t onehot_bf16x4(float x, uint2 m) {
+  const unsigned p = cvt_pk_bf16(x, x);
+  return __builtin_bit_cast(s16x4_t, make_uint2(p & m.x, p & m.y));
 }
 
 // Two-term bf16 split of fp32 values: x = hi + lo + O(2^-18 |x|), hi = bf16(x), lo = bf16(x - hi)
@@ -165,12 +172,22 @@ __device__ __forceinline__ void split_bf16x4(float a, float b, float c, float d,
   lo = __builtin_bit_cast(s16x4_t, make_uint2(cvt_pk_bf16(a - ha, b - hb), cvt_pk_bf16(c - hc, d - hd)));
 }
 
+// The split of x placed as a one-hot operand pair at element e (shifts of 16 e bits).
 __device__ __forceinline__ void split_onehot_bf16x4(float x, int e, s16x4_t& hi, s16x4_t& lo) {
   const __bf16 hb = (__bf16)x;
   const __bf16 lb = (__bf16)(x - (float)hb);
   const int sh = 16 * e;
   hi = __builtin_bit_cast(s16x4_t, (unsigned long long)__builtin_bit_cast(unsigned short, hb) << sh);
   lo = __builtin_bit_cast(s16x4_t, (unsigned long long)__builtin_bit_cast(unsigned short, lb) << sh);
+}
+
+// The split of x placed as a one-hot operand pair (masks of onehot_masks(e)).
+__device__ __forceinline__ void split_onehot_bf16x4(float x, uint2 m, s16x4_t& hi, s16x4_t& lo) {
+  const unsigned p = cvt_pk_bf16(x, x);
+  const float r = x - __uint_as_float(p << 16);
+  const unsigned q = cvt_pk_bf16(r, r);
+  hi = __builtin_bit_cast(s16x4_t, make_uint2(p & m.x, p & m.y));
+  lo = __builtin_bit_cast(s16x4_t, make_uint2(q & m.x, q & m.y));
 }
 
 // B operand of v_mfma_f32_16x16x32_bf16 for a diagonal weight matrix stacked as [hi; lo] along k:
