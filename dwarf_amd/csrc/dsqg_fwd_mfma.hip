@@ -91,16 +91,30 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   load_sparse_deltas(p.taps, dl_s);
 
   // ---- Global loads (all zero-filled outside [0, N) by the buffer range check). ----
-  // scale_embed and the band's query operand go first: the T table waits for them alone.
+  // The query rows go first (the band waits for them): with scale_embed the scale_embed rows
+  // and the band's B operand (query rows in the MFMA operand order, for the T table), and in
+  // both variants the query rows in the row-chunk layout (whole rows per D/8 lanes).  Without
+  // scale_embed the B operand is read back from that copy, staged in the wave's block after the
+  // window barrier (free until the long-range P V), which saves the operand-order global loads
+  // (16 rows x 16 B per 16 lanes); with it, the T table needs the operand before the window.
+  int qlaneR[CHW], klaneR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
+    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
+  }
   SeRows<D> seR;
   if constexpr (HAS_SE) seR.load(p.scale_embed, J, tid);
-  const int qlane = opaque(i * qsn + 8 * g);
   bf16x8_t qB[KS];
   if constexpr (HAS_SE) {
+    const int qlane = opaque(i * qsn + 8 * g);
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (8 * g + 32 * s < D ? qlane + 32 * s : kNoElem)));
   }
+  uint4 qR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
   // Offsets are (uniform row) * stride + (per-lane part), so the row products stay scalar.
   uint4 wv[CWIN], wk[CWIN];
 #pragma unroll
@@ -110,22 +124,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
     wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
   }
-  // The band's B operand (query rows in the MFMA operand order): with scale_embed loaded from
-  // global memory above (the T table needs it first); without, read after the window barrier
-  // from the whole-row copy below, staged in the wave's block (free until the long-range P V),
-  // which saves the operand-order global loads (16 rows x 16 B per 16 lanes).
-  // The same query rows and the long-range key rows n0w - delta + 0..15 in the row-chunk
-  // layout (whole rows per 8 lanes); the keys in two halves (the second after the dense band has
-  // consumed its registers) to bound the register peak.
-  int qlaneR[CHW], klaneR[CHW];
-#pragma unroll
-  for (int u = 0; u < CHW; ++u) {
-    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
-    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
-  }
-  uint4 qR[CHW];
-#pragma unroll
-  for (int u = 0; u < CHW; ++u) qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
+  // The long-range key rows n0w - delta + 0..15 in the row-chunk layout, in two halves (the
+  // second after the dense band has consumed its registers) to bound the register peak.
   constexpr int NH = (NSM + 1) / 2;
   uint4 kS[NSM][CHW];
 #pragma unroll
