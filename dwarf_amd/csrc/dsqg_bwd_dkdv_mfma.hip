@@ -257,11 +257,15 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
       }
     }
   }
-  const bool sel_hi = g == (i >> 3), sel_lo = g == 2 + (i >> 3);
+  // One-hot weights of the long-range taps: key i's weight in the diagonal lane (i, i / 4),
+  // element i % 4 (the B operand of the 16x16x16 products below); other lanes contribute zeros.
+  const bool diag = g == (i >> 2);
   // The wave's long-range query / dOut rows are staged in the window tiles (rows 16w..16w+15),
   // free once every wave's band is done.
   bf16_t* qsw = sQ + w * 16 * RV;
   bf16_t* osw = sO + w * 16 * RV;
+  const bf16_t* qtr = qsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+  const bf16_t* otr = osw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
   __syncthreads();  // every wave's band reads of sQ / sO are done
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
@@ -304,16 +308,22 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
       __builtin_amdgcn_wave_barrier();
       const float2 pr = sPair[w][i];
       const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
-      const bool ok = key_ok && nq < N;  // every lane of column i: the stacked operand below
+      const bool ok = key_ok && nq < N;
       const float uval = pr.y;
       const float alpha = ok ? __builtin_amdgcn_exp2f(pr.x + sBias2[j] - lseq) : 0.f;
       const float dS = a * alpha * (uval - dpq);
-      const bf16x8_t bk = onehot_hilo_bf16x8(sGainC[j] * dS, sel_hi, sel_lo, i & 7);
-      const bf16x8_t bv = onehot_hilo_bf16x8(a * alpha, sel_hi, sel_lo, i & 7);
+      // The weights as bf16 hi + lo pairs (fp32 precision of the products); each transposed
+      // read of the staged rows feeds two 16x16x16 products, hi and lo.
+      s16x4_t bk, bkl, bv, bvl;
+      split_onehot_bf16x4(diag ? sGainC[j] * dS : 0.f, i & 3, bk, bkl);
+      split_onehot_bf16x4(diag ? a * alpha : 0.f, i & 3, bv, bvl);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        dK[db] = mfma_16x16x32(lds_read_tr16_stacked(qsw, RV, i, g, 16 * db), bk, dK[db]);
-        dV[db] = mfma_16x16x32(lds_read_tr16_stacked(osw, RV, i, g, 16 * db), bv, dV[db]);
+        const s16x4_t qt = lds_read_tr16(qtr + 16 * db), ot = lds_read_tr16(otr + 16 * db);
+        dK[db] = mfma_16x16x16(qt, bk, dK[db]);
+        dK[db] = mfma_16x16x16(qt, bkl, dK[db]);
+        dV[db] = mfma_16x16x16(ot, bv, dV[db]);
+        dV[db] = mfma_16x16x16(ot, bvl, dV[db]);
       }
     }
   }

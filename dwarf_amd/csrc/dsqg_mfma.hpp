@@ -190,35 +190,6 @@ __device__ __forceinline__ void split_onehot_bf16x4(float x, uint2 m, s16x4_t& h
   lo = __builtin_bit_cast(s16x4_t, make_uint2(q & m.x, q & m.y));
 }
 
-// B operand of v_mfma_f32_16x16x32_bf16 for a diagonal weight matrix stacked as [hi; lo] along k:
-// column i holds bf16(x) at k = i and bf16(x - bf16(x)) at k = 16 + i (lane (i, g) holds
-// k = 8g .. 8g+7).  Paired with an A operand whose k and k + 16 read the same row, one MFMA adds
-// row i times x at fp32 precision.
-__device__ __forceinline__ bf16x8_t onehot_hilo_bf16x8(float x, bool sel_hi, bool sel_lo, int e) {
-  const __bf16 hb = (__bf16)x;
-  const __bf16 lb = (__bf16)(x - (float)hb);
-  const unsigned v = sel_hi ? (unsigned)__builtin_bit_cast(unsigned short, hb)
-                            : (sel_lo ? (unsigned)__builtin_bit_cast(unsigned short, lb) : 0u);
-  const unsigned word = v << (16 * (e & 1));
-  const int dw = e >> 1;
-  uint4 r;
-  r.x = dw == 0 ? word : 0u;
-  r.y = dw == 1 ? word : 0u;
-  r.z = dw == 2 ? word : 0u;
-  r.w = dw == 3 ? word : 0u;
-  return __builtin_bit_cast(bf16x8_t, r);
-}
-
-// A operand of v_mfma_f32_16x16x32_bf16 from a row-major bf16 block (row stride rs elements):
-// lane (i, g) receives column c0 + i of rows 8 (g & 1) + 0..7, so k and k + 16 see the same row.
-__device__ __forceinline__ bf16x8_t lds_read_tr16_stacked(const bf16_t* blk, int rs, int i, int g, int c0) {
-  const bf16_t* p0 = blk + (8 * (g & 1) + (i >> 2)) * rs + c0 + 4 * (i & 3);
-  const s16x4_t a = lds_read_tr16(p0), b = lds_read_tr16(p0 + 4 * rs);
-  typedef short s16x8_t __attribute__((ext_vector_type(8)));
-  const s16x8_t r = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
-  return __builtin_bit_cast(bf16x8_t, r);
-}
-
 // fp32 value -> (bf16 hi, bf16 lo) element pair for staging a matrix in two LDS planes.
 __device__ __forceinline__ void split_bf16(float x, bf16_t& hi, bf16_t& lo) {
   const __bf16 hb = (__bf16)x;
