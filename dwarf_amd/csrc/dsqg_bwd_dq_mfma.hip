@@ -16,9 +16,9 @@
 // dS is then written to a per-wave [query][tap] table in LDS, from which the workgroup sums
 // dbias (and dg, da) in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS over
 // the tile's 64 queries, its [D x J] output tiles split over the four waves).
-// With scale_embed the q.se_j term of the dense taps is an MFMA (SE Q^T) filed in a per-wave
-// [query][tap] table that shares the wave's staging block; for the long-range taps it is a VALU
-// dot product folded into the score, like q.k.  scale_embed is staged as two bf16 planes
+// With scale_embed the q.se_j term is an MFMA (SE Q^T): for the dense taps filed in a per-wave
+// [query][tap] table that shares the wave's staging block, for the long-range taps in their dS
+// table slots until the diagonal lane reads them.  scale_embed is staged as two bf16 planes
 // (hi = bf16(se), lo = bf16(se - hi)), and every weight that enters an MFMA (the dense band's
 // and the one-hot long-range X / Y weights, dS in dse and in SE^T dS^T) is split the same way,
 // so these products keep fp32 precision as in the reference (kernels/dsqg_attention_v3.py:
