@@ -16,7 +16,7 @@ PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("DSQG_HIP_LIB", PKG_DIR / "libdsqg_hip.so"))
 
 MAX_OFFSETS = 64
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DSQG_OK, DSQG_EINVAL, DSQG_EUNSUPPORTED, DSQG_EHIP, DSQG_EWORKSPACE = 0, 1, 2, 3, 4
 DSQG_ETOOLARGE = 5

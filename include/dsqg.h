@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define DSQG_ABI_VERSION 1
+#define DSQG_ABI_VERSION 2
 #define DSQG_MAX_OFFSETS 64
 
 /* Same type as hipStream_t; NULL is the null stream. */
