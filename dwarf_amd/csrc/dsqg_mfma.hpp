@@ -16,7 +16,6 @@
 namespace dsqg {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -188,13 +187,6 @@ __device__ __forceinline__ void split_onehot_bf16x4(float x, uint2 m, s16x4_t& h
   const unsigned q = cvt_pk_bf16(r, r);
   hi = __builtin_bit_cast(s16x4_t, make_uint2(p & m.x, p & m.y));
   lo = __builtin_bit_cast(s16x4_t, make_uint2(q & m.x, q & m.y));
-}
-
-// fp32 value -> (bf16 hi, bf16 lo) element pair for staging a matrix in two LDS planes.
-__device__ __forceinline__ void split_bf16(float x, bf16_t& hi, bf16_t& lo) {
-  const __bf16 hb = (__bf16)x;
-  hi = __builtin_bit_cast(bf16_t, hb);
-  lo = __builtin_bit_cast(bf16_t, (__bf16)(x - (float)hb));
 }
 
 // scale_embed [J, D] (fp32, 16-byte aligned) as 48 rows x DP bf16 in LDS (row stride RV; rows
