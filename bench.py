@@ -113,8 +113,9 @@ def cpu_baseline_decode(steps=10):
             "ms_per_step": round(dt * 1e3, 3)}
 
 
-def bench_decode(dev, steps=1000, layers=8):
-    """Ring-buffer decode step, workload 4 (B256 H12 D64, 44 offsets, 1537-slot rings).
+def bench_decode(dev, steps=1000, layers=8, batch=None):
+    """Ring-buffer decode step, workload 4 (B256 H12 D64, 44 offsets, 1537-slot rings; `batch`
+    replaces B for the batch sweep).
 
     Two figures, both from HIP-graph replays timed with HIP events:
     * ``layers`` (the headline): ``layers`` independent ring pairs, as the caches of an
@@ -128,7 +129,7 @@ def bench_decode(dev, steps=1000, layers=8):
     from dwarf_amd import ops
     from dwarf_amd.workloads import DECODE, decode_bytes_per_step, make_decode_inputs
     cfg = DECODE
-    B, H, D, S = cfg["B"], cfg["H"], cfg["D"], cfg["S"]
+    B, H, D, S = batch or cfg["B"], cfg["H"], cfg["D"], cfg["S"]
     offs = list(cfg["offsets"])
     small = make_decode_inputs(device="cpu", B=B, H=H, D=D, S=2)  # q, k_new, v_new, pos, bias
     gen = torch.Generator(device=dev).manual_seed(4004)
@@ -252,6 +253,40 @@ def bench_module(dev, steps=20, warmup=20):
             fn(i)
         res[f"ms_{name}"] = round(_events_ms(fn, steps, stream), 4)
     return res
+
+
+def decode_sweep(dev, steps):
+    """Decode step time against batch size (the fixed per-step latency and the marginal
+    bandwidth), next to the per-launch time of a trivial kernel replayed from a hipGraph."""
+    import torch
+    rows = []
+    for B in (32, 64, 128, 256, 512):
+        r = bench_decode(dev, steps=steps, batch=B)
+        rows.append({"B": B, "us_per_step": r["us_per_step"],
+                     "algorithmic_bytes_per_step": r["algorithmic_bytes_per_step"],
+                     "frac_hbm_peak": r["frac_hbm_peak"]})
+        print(f"[bench] decode B{B}: {r['us_per_step']} us", file=sys.stderr, flush=True)
+    x = torch.zeros(64, device=dev)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        x.add_(1)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        for _ in range(steps):
+            x.add_(1)
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    e1.synchronize()
+    trivial = round(e0.elapsed_time(e1) * 1000.0 / steps, 3)
+    print(json.dumps({"decode_sweep": rows, "trivial_kernel_us_per_launch": trivial}), flush=True)
+    return 0
 
 
 def bench_pool(dev, steps=200, sets=3):
@@ -621,6 +656,9 @@ def main(argv=None):
     ap.add_argument("--probes", action="store_true",
                     help="run the memory-system probes (bench_probes.hip) and exit with their JSON line")
     ap.add_argument("--copy-mib", type=int, default=256)
+    ap.add_argument("--decode-sweep", action="store_true",
+                    help="time the decode step (8 ring pairs) at batch 32..512 and a trivial "
+                         "graph-replayed kernel, print one JSON line and exit")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -646,6 +684,8 @@ def main(argv=None):
         return profile_mode(args, w, dev)
     if args.probes:
         return run_probes(dev)
+    if args.decode_sweep:
+        return decode_sweep(dev, args.decode_steps)
 
     sets = make_sets(w, dev, args.sets)
 
