@@ -23,8 +23,6 @@ constexpr int lanes_per_row(int D) { return D <= 32 ? 4 : (D <= 64 ? 8 : 16); }
 // Element conversion.  bf16 is the upper half of an IEEE binary32; float -> bf16 rounds to
 // nearest-even (NaN stays a quiet NaN).
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
-
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
