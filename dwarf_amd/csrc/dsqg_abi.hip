@@ -1,7 +1,7 @@
 // C ABI of libdsqg_hip.so (declared in include/dsqg.h).  Every entry point validates its
 // arguments on the host before touching HIP, then fills a launch parameter block and
-// dispatches on (dtype, head dim, offset count).  No allocation, no synchronisation, no
-// mutable global state.
+// dispatches on (dtype, head dim, offset count).  No allocation and no synchronisation; the
+// only mutable global state is dsqg_bwd_noalloc's per-device static scratch (end of file).
 #include <limits.h>
 #include <math.h>
 #include <string.h>

@@ -15,8 +15,9 @@
  * Conventions.
  *  - Every entry point returns a dsqg_status.  Argument checks happen on the host before any
  *    HIP call, so a bad call never launches a kernel.
- *  - The library never allocates device memory, never synchronises, and keeps no mutable
- *    global state: it is re-entrant, and all work is ordered on the stream passed in.
+ *  - The library never allocates device memory and never synchronises; all work is ordered on
+ *    the stream passed in.  Its only mutable global state is dsqg_bwd_noalloc's per-device
+ *    static scratch (below); every other entry point is re-entrant.
  *  - Tensor pointers are device pointers.  Element strides are int64 element counts, in the
  *    order [B,H,N,D]; the innermost (D) stride must be 1 and the other strides and the base
  *    pointers must keep every row 16-byte aligned.
