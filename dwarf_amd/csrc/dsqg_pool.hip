@@ -220,22 +220,31 @@ __device__ __forceinline__ void rl_exclusive_scan(float (&v)[kCpl], float* sW) {
   }
 }
 
-// Sum over chunks k = first, first + 16, ... < end of a [B][nchunks][C] partial array.
-__device__ __forceinline__ void strided_chunk_sum(const float* part, const PoolParams& p,
-                                                  const PoolLane& q, int first, int end,
-                                                  float (&acc)[kCpl]) {
-#pragma unroll
-  for (int e = 0; e < kCpl; ++e) acc[e] = 0.f;
-  if (!q.active) return;
-#pragma unroll 4
-  for (int k = first; k < end; k += kPoolRl) {
-    float v[kCpl];
-    const float4 a = *reinterpret_cast<const float4*>(part + ((long long)q.b * p.nchunks + k) * p.C + q.c);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-#pragma unroll
-    for (int e = 0; e < kCpl; ++e) acc[e] += v[e];
+// Sum over chunks k = first, first + 16, ... < last of a [B][nchunks][C] partial array, in
+// two steps: begin() issues the first two loads (chunks first, first + 16) so
+// that they travel with the row loads that follow, finish() adds them and any further chunks.
+struct ChunkCarry {
+  float4 a0, a1;
+  int next, end;
+  __device__ __forceinline__ void begin(const float* part, const PoolParams& p, const PoolLane& q,
+                                        int first, int last) {
+    end = q.active ? last : first;
+    const float* base = part + (long long)q.b * p.nchunks * p.C + q.c;
+    a0 = first < end ? *reinterpret_cast<const float4*>(base + (long long)first * p.C) : make_float4(0.f, 0.f, 0.f, 0.f);
+    a1 = first + kPoolRl < end ? *reinterpret_cast<const float4*>(base + (long long)(first + kPoolRl) * p.C)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+    next = first + 2 * kPoolRl;
   }
-}
+  __device__ __forceinline__ void finish(const float* part, const PoolParams& p, const PoolLane& q,
+                                         float (&acc)[kCpl]) const {
+    acc[0] = a0.x + a1.x; acc[1] = a0.y + a1.y; acc[2] = a0.z + a1.z; acc[3] = a0.w + a1.w;
+    const float* base = part + (long long)q.b * p.nchunks * p.C + q.c;
+    for (int k = next; k < end; k += kPoolRl) {
+      const float4 a = *reinterpret_cast<const float4*>(base + (long long)k * p.C);
+      acc[0] += a.x; acc[1] += a.y; acc[2] += a.z; acc[3] += a.w;
+    }
+  }
+};
 
 // ---- Pass 1: chunk sums of x (and, backward, of dout * s / (n+1)). -----------------------
 template <int RPL, bool BWD>
@@ -282,6 +291,8 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
   const PoolLane q = pool_lane<RPL>(p);
   const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
   const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+  ChunkCarry cc;
+  cc.begin(p.px, p, q, q.rl, q.chunk);
   float x[RPL][kCpl], s[RPL][kCpl];
   float run[kCpl];
 #pragma unroll
@@ -298,7 +309,7 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
     }
   }
   float carry[kCpl];
-  strided_chunk_sum(p.px, p, q, q.rl, q.chunk, carry);
+  cc.finish(p.px, p, q, carry);
   rl_total(carry, sW);
   rl_exclusive_scan<false>(run, sW);
 #pragma unroll
@@ -326,6 +337,9 @@ __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) 
   const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
   const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
   const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
+  ChunkCarry ccx, ccp;
+  ccx.begin(p.px, p, q, q.rl, q.chunk);
+  ccp.begin(p.pp, p, q, q.chunk + 1 + q.rl, p.nchunks);
   float x[RPL][kCpl], s[RPL][kCpl], y[RPL][kCpl];
   float runx[kCpl], runp[kCpl];
 #pragma unroll
@@ -347,8 +361,8 @@ __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) 
     }
   }
   float cx[kCpl], cp[kCpl];
-  strided_chunk_sum(p.px, p, q, q.rl, q.chunk, cx);
-  strided_chunk_sum(p.pp, p, q, q.chunk + 1 + q.rl, p.nchunks, cp);
+  ccx.finish(p.px, p, q, cx);
+  ccp.finish(p.pp, p, q, cp);
   rl_total(cx, sW);
   rl_total(cp, sW);
   rl_exclusive_scan<false>(runx, sW);
