@@ -441,6 +441,8 @@ def profile_mode(args, w, dev):
     from dwarf_amd.workloads import make_inputs
     if args.profile_kernel == "decode":
         return profile_decode(args, dev)
+    if args.profile_kernel == "pool":
+        return profile_pool(args, dev)
     if args.profile_se:  # the scale_embed leg's inputs (scale_embed and if_gain)
         _, d, fl, bl = make_sets(w, dev, 1, scale_embed=True, if_gain=True)[0]
     else:
@@ -468,6 +470,28 @@ def profile_mode(args, w, dev):
     torch.cuda.synchronize()
     print(f"[bench] profile mode: {args.profile_reps} launches of {args.profile_kernel}, "
           f"{args.profile_reps} copies of {nbytes} bytes", file=sys.stderr, flush=True)
+    return 0
+
+
+def profile_pool(args, dev):
+    """The pool leg's shape (x, gate_pre, dout [8, 2048, 768] bf16): one forward and one
+    backward first, then --profile-reps of each (two launches apiece)."""
+    import torch
+    from dwarf_amd import ops
+    B, N, C = 8, 2048, 768
+    g = torch.Generator().manual_seed(2024)
+    x, gp, dy = ((torch.randn((B, N, C), generator=g) * sc).to(dev, torch.bfloat16)
+                 for sc in (1.0, 2.0, 1.0))
+    fwd, bwd = ops.PoolLaunch(x, gp), ops.PoolLaunch(x, gp, dy)
+    fwd.run()
+    bwd.run()
+    torch.cuda.synchronize()
+    for _ in range(args.profile_reps):
+        fwd.run()
+        bwd.run()
+    torch.cuda.synchronize()
+    print(f"[bench] profile mode: {args.profile_reps} pool forward + backward calls", file=sys.stderr,
+          flush=True)
     return 0
 
 
@@ -646,10 +670,11 @@ def main(argv=None):
     ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
     ap.add_argument("--no-pool", action="store_true", help="skip the interference-pool leg")
     ap.add_argument("--no-generation", action="store_true", help="skip the generation leg")
-    ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv", "decode"], default=None,
+    ap.add_argument("--profile-kernel", choices=["fwd", "dq", "dkdv", "decode", "pool"], default=None,
                     help="counter-collection mode: launch only this kernel --profile-reps times, "
                          "plus a plain device copy of --copy-mib MiB (the scale reference for "
-                         "FETCH_SIZE / WRITE_SIZE), then exit without a JSON line")
+                         "FETCH_SIZE / WRITE_SIZE; 'pool': its forward and backward, no copy), "
+                         "then exit without a JSON line")
     ap.add_argument("--profile-reps", type=int, default=5)
     ap.add_argument("--profile-se", action="store_true",
                     help="with --profile-kernel: the scale_embed leg's inputs (scale_embed, if_gain)")

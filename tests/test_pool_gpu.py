@@ -61,10 +61,11 @@ def _inputs(B, N, C, xdt, gdt, seed):
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 8), (2, 37, 24), (3, 300, 256), (2, 2048, 512),
-                                   (1, 5000, 64)])
+                                   (1, 5000, 64), (4, 1100, 1032)])
 @pytest.mark.parametrize("xdt,gdt", [(F32, F32), (F32, F16), (BF16, BF16), (F16, F16)])
 def test_pool_gate_matches_oracle(gpu_device, shape, xdt, gdt):
-    """Forward and both gradients through the autograd op, ragged N and C included."""
+    """Forward and both gradients through the autograd op, ragged N and C included (the last
+    shape: N and C off every power of two, 17 workgroup columns of 64 channels)."""
     B, N, C = shape
     _say(f"shape={shape} x={xdt} gate={gdt}")
     x, gp, dy = _inputs(B, N, C, xdt, gdt, seed=B * 7919 + N)
@@ -138,12 +139,14 @@ def test_pool_gate_deterministic(gpu_device):
     assert torch.equal(da[0], db[0]) and torch.equal(da[1], db[1])
 
 
-def test_pool_gate_large_properties(gpu_device):
+@pytest.mark.parametrize("shape", [(2, 100_000, 64), (2, 16_384, 2048)])
+def test_pool_gate_large_properties(gpu_device, shape):
     """At sizes the float64 oracle would be slow on: constant input gives pool == 1 exactly
     (sums of ones are exact in fp32), so out == sigmoid(gate); the last row times N / s is the
-    column total; dx for dout = 1 at gate 0 is 0.5 * (H_N - H_m)."""
-    B, N, C = 2, 100_000, 64
-    _say(f"large N={N}")
+    column total; dx for dout = 1 at gate 0 is 0.5 * (H_N - H_m).  Long columns, then wide
+    rows."""
+    B, N, C = shape
+    _say(f"large shape={shape}")
     ones = torch.ones((B, N, C), device=gpu_device)
     g = torch.Generator(device="cpu").manual_seed(8)
     gp = torch.randn((B, N, C), generator=g).to(gpu_device)
