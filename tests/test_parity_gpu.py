@@ -191,6 +191,19 @@ def test_other_offset_tables_bf16(gpu_device, offsets, N):
     compare(got, ref, "bf16")
 
 
+@pytest.mark.parametrize("offsets,N", [(OFFSETS_J46, 3100), (OFFSETS_J47, 4097)])
+def test_long_tables_with_scale_embed(gpu_device, offsets, N):
+    """The N=4096 trainers' call (train/train_4096_13m_condU.py:102-105): pos_bias and scale_embed
+    over the 46- and 47-offset tables at D=64 with the IF gain and no score gain, which selects
+    the scale_embed kernels for 13 and 14 long-range taps."""
+    inp = _rand_inputs(1, 2, N, 64, offsets, torch.bfloat16, seed=len(offsets) + 7, gains=False)
+    inp["if_gain"] = torch.rand(2, generator=torch.Generator().manual_seed(len(offsets))) * 0.4 + 0.8
+    _say(f"bf16 offsets J={len(offsets)} N={N} + scale_embed")
+    got = gpu_run(inp, offsets, gpu_device)
+    ref = oracle_chunked(inp, offsets, torch.float32)
+    compare(got, ref, "bf16", case=f"J={len(offsets)} + scale_embed")
+
+
 def test_bf16_table_beyond_the_mfma_kernels_is_rejected(gpu_device):
     """bf16 has one implementation: a table with more than 16 taps beyond the dense window
     (here 47) is refused with DSQG_EUNSUPPORTED before any launch; fp32 still takes it."""
