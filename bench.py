@@ -255,6 +255,59 @@ def bench_module(dev, steps=20, warmup=20):
     return res
 
 
+def table_sweep(dev, reps=50):
+    """Each attention kernel at the config-2 shape (B8 H12 N2048 D64 bf16) over four offset
+    tables: delta = 0 alone (the kernels' fixed structure: window staging, band tiles,
+    epilogue), the dense window 0..32, delta = 0 with the eleven long-range taps, and the full
+    44-offset table.  Isolated launches (fwd, dq phase, dk/dv phase) timed with HIP events over
+    two alternating input sets; medians of `reps`.  Prints one JSON line."""
+    import torch
+    from dwarf_amd import ops
+    from dwarf_amd.offsets import OFFSETS_V3
+    B, H, N, D = 8, 12, 2048, 64
+    lr = tuple(o for o in OFFSETS_V3 if o > 32)
+    tables = [("delta 0", (0,)), ("dense 0..32", tuple(range(33))), ("0 + 11 long-range", (0,) + lr),
+              ("V3 (44)", tuple(OFFSETS_V3))]
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev).manual_seed(77)
+    rows = []
+    for name, offs in tables:
+        J = len(offs)
+        sets = []
+        for _ in range(2):
+            q, k, v, do = (torch.randn((B, H, N, D), generator=gen, device=dev).to(torch.bfloat16)
+                           for _ in range(4))
+            pb = torch.randn((J, H), generator=gen, device=dev) * 0.5
+            fl = ops.FwdLaunch(q, k, v, pb, None, None, None, list(offs))
+            fl.run()
+            bl = ops.BwdLaunch(q, k, v, do, fl.lse, pb, None, None, None, list(offs), False, False, False)
+            sets.append((fl, bl))
+        for i in range(10):
+            sets[i % 2][0].run()
+            sets[i % 2][1].run()
+        times = {"fwd": [], "dq": [], "dkdv": []}
+        for i in range(reps):
+            fl, bl = sets[i % 2]
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            e[0].record(stream)
+            fl.run()
+            e[1].record(stream)
+            bl.run("dq")
+            e[2].record(stream)
+            bl.run("dkdv")
+            e[3].record(stream)
+            e[3].synchronize()
+            for j, key in enumerate(("fwd", "dq", "dkdv")):
+                times[key].append(e[j].elapsed_time(e[j + 1]) * 1000.0)
+        row = {"table": name, "J": J}
+        row.update({f"{key}_us": round(statistics.median(v), 2) for key, v in times.items()})
+        rows.append(row)
+        print(f"[bench] table {name}: {row}", file=sys.stderr, flush=True)
+        del sets
+    print(json.dumps({"table_sweep": rows, "shape": f"B{B} H{H} N{N} D{D} bf16"}), flush=True)
+    return 0
+
+
 def decode_sweep(dev, steps):
     """Decode step time against batch size (the fixed per-step latency and the marginal
     bandwidth), next to the per-launch time of a trivial kernel replayed from a hipGraph."""
@@ -684,6 +737,10 @@ def main(argv=None):
     ap.add_argument("--decode-sweep", action="store_true",
                     help="time the decode step (8 ring pairs) at batch 32..512 and a trivial "
                          "graph-replayed kernel, print one JSON line and exit")
+    ap.add_argument("--table-sweep", action="store_true",
+                    help="time fwd, dq and dk/dv at the config-2 shape over four offset tables "
+                         "(delta 0 alone, dense 0..32, delta 0 + 11 long-range, V3), print one "
+                         "JSON line and exit")
     args = ap.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -711,6 +768,8 @@ def main(argv=None):
         return run_probes(dev)
     if args.decode_sweep:
         return decode_sweep(dev, args.decode_steps)
+    if args.table_sweep:
+        return table_sweep(dev)
 
     sets = make_sets(w, dev, args.sets)
 

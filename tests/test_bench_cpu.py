@@ -24,7 +24,7 @@ def test_more_than_one_gpu_is_refused(capsys):
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU exit")
-@pytest.mark.parametrize("argv", [[], ["--decode-sweep"], ["--profile-kernel", "pool"],
+@pytest.mark.parametrize("argv", [[], ["--decode-sweep"], ["--table-sweep"], ["--profile-kernel", "pool"],
                                   ["--profile-kernel", "dq", "--profile-se"], ["--probes"]])
 def test_every_mode_needs_a_gpu(capsys, argv):
     assert _bench().main(argv) == 1
