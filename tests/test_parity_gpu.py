@@ -191,6 +191,19 @@ def test_other_offset_tables_bf16(gpu_device, offsets, N):
     compare(got, ref, "bf16")
 
 
+def test_long_sequence(gpu_device):
+    """A sequence of 100,003 tokens (ragged: the last tile holds 35 rows), bf16 with scale_embed
+    and the IF gain: row offsets far beyond the workloads' (N * row bytes = 12.8 MB per slice),
+    every tap valid for almost all rows."""
+    N = 100_003
+    inp = _rand_inputs(1, 2, N, 64, OFFSETS_V3, torch.bfloat16, seed=N, gains=False)
+    inp["if_gain"] = torch.tensor([0.9, 1.1])
+    _say(f"bf16 long sequence N={N}")
+    got = gpu_run(inp, OFFSETS_V3, gpu_device)
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float32)
+    compare(got, ref, "bf16", case=f"N={N} + scale_embed")
+
+
 @pytest.mark.parametrize("offsets,N", [(OFFSETS_J46, 3100), (OFFSETS_J47, 4097)])
 def test_long_tables_with_scale_embed(gpu_device, offsets, N):
     """The N=4096 trainers' call (train/train_4096_13m_condU.py:102-105): pos_bias and scale_embed
