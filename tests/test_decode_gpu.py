@@ -179,6 +179,27 @@ def test_decode_other_offset_tables(gpu_device, offsets, p, dtype):
         assert _bf16_ratio(out, ref) <= 1.0
 
 
+def test_decode_positions_beyond_32_bits(gpu_device):
+    """Positions at and past 2^31 (the kernel takes p mod S in 64-bit arithmetic there) next to
+    an ordinary one: output and ring writes equal the oracle's step, three steps in a row."""
+    B, H, D, S = 4, 2, 64, 1537
+    inp = make_decode_inputs(B=B, H=H, D=D, S=S, seed=23)
+    d = {k: v.to(gpu_device) for k, v in inp.items()}
+    k_ref, v_ref = inp["k_ring"].clone(), inp["v_ring"].clone()
+    pos = torch.tensor([2 ** 31 - 2, 2 ** 31 + 5, 3_000_000_000_123, 1536], dtype=torch.int64)
+    g = torch.Generator().manual_seed(5)
+    for step in range(3):
+        q, kn, vn = (torch.randn(B, H, D, generator=g).to(torch.bfloat16) for _ in range(3))
+        out = ops.dsqg_decode(q.to(gpu_device), kn.to(gpu_device), vn.to(gpu_device),
+                              d["k_ring"], d["v_ring"], pos.to(gpu_device), d["pos_bias"],
+                              None, None, None, list(OFFSETS_V3)).cpu()
+        ref = decode_step(q.float(), kn.float(), vn.float(), k_ref, v_ref, pos, inp["pos_bias"])
+        _say(f"step {step} positions {pos.tolist()}: err {_err(out, ref)[0]:.3e}")
+        assert _bf16_ratio(out, ref) <= 1.0
+        assert torch.equal(d["k_ring"].cpu(), k_ref) and torch.equal(d["v_ring"].cpu(), v_ref)
+        pos = pos + 1
+
+
 def test_decode_negative_position_stays_invalid_over_replays(gpu_device):
     """A negative position gives a NaN output row, leaves that sequence's rings untouched, and
     writes the same negative value to pos_next, so a pos / pos_next ping-pong replay keeps the
