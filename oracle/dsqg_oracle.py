@@ -39,7 +39,7 @@ invariance, sum_j dbias = 0, causality).
 from __future__ import annotations
 
 import math
-from typing import Optional, Sequence
+from typing import Sequence
 
 import torch
 import torch.nn.functional as F

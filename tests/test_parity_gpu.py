@@ -10,8 +10,6 @@ Masking (n - delta < 0) is exercised at every N below max(delta) and by rows 0..
 full-size configs.
 """
 
-import math
-
 import pytest
 import torch
 
