@@ -95,34 +95,17 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   const bool lane_ok = d0 < D;
   const int J = p.taps.J, S = p.S;
   const float c = p.scale;
-  const long long pos = p.pos[b];
+  const long long pos = p.pos[b];  // waited for at the validity test below
   T* outrow = static_cast<T*>(p.out) + bh * D;
-  if (pos < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
-    if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
-    if (lane < G && lane_ok) {
-      float o[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = __int_as_float(0x7fc00000);
-      Vec8<T>::store(outrow + d0, o);
-    }
-    return;
-  }
-  if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos + 1;
-
   const T* qrow = static_cast<const T*>(p.q) + bh * D;
   const T* knew = static_cast<const T*>(p.k_new) + bh * D;
   const T* vnew = static_cast<const T*>(p.v_new) + bh * D;
-  T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
-  T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
-  // Ring reads go through buffer resources over this sequence's ring: a masked tap gets an
-  // offset past the end and reads zeros, so it needs no select in the weighted sum.
-  const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(kring, (short)0, S * D * E, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(vring, (short)0, S * D * E, 0x00020000);
 
-  // Two memory round trips per step: everything that does not depend on the position (query,
-  // new key/value row, per-tap bias and gain) goes out together with the position itself; the
-  // ring rows of the taps follow, all requested before any arithmetic.  Tap 0 (delta = 0) is
-  // the new row, already in registers; so is the row written into the ring.
+  // Two memory round trips per step.  Everything that does not depend on the position (query,
+  // new key/value row, per-tap bias, gain and scale_embed) is requested before the position is
+  // waited for, and with scale_embed each pass's share of q.se_j is formed meanwhile; the ring
+  // rows of the taps follow the position, all requested before the rest of the arithmetic.
+  // Tap 0 (delta = 0) is the new row, already in registers; so is the row written into the ring.
   constexpr int C16 = E == 4 ? 2 : 1;  // 16-byte chunks per lane (8 elements)
   uint4 qraw[C16], knraw[C16], vnraw[C16];
 #pragma unroll
@@ -139,6 +122,45 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     pbias[t] = p.pos_bias[jj * p.H + h];
     pgain[t] = p.score_gain ? p.score_gain[h * J + jj] : 1.0f;
   }
+  float q[8];
+  Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
+  float sed[P];  // this lane's share of q.se_j for the pass-t tap (summed over the row with q.k)
+  if constexpr (HAS_SE) {
+    float sev[P][8];
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      const int j = t * R + r;
+      const int jj = j < J ? j : 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sev[t][e] = lane_ok ? p.scale_embed[jj * D + d0 + e] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = fmaf(q[e], sev[t][e], acc);
+      sed[t] = acc;
+    }
+  }
+
+  if (pos < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
+    if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
+    if (lane < G && lane_ok) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = __int_as_float(0x7fc00000);
+      Vec8<T>::store(outrow + d0, o);
+    }
+    return;
+  }
+  if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos + 1;
+
+  T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
+  T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
+  // Ring reads go through buffer resources over this sequence's ring: a masked tap gets an
+  // offset past the end and reads zeros, so it needs no select in the weighted sum.
+  const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(kring, (short)0, S * D * E, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(vring, (short)0, S * D * E, 0x00020000);
 
   // Slot of tap delta: (pos mod S) - delta, wrapped once (0 < delta < S).  The new row goes
   // into slot pos mod S now: no tap of this step reads that slot.
@@ -171,13 +193,9 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     }
   }
 
-  float q[8];
-  if constexpr (E == 4) Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
   float s[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) {
-    const int j = t * R + r;
-    const int jj = j < J ? j : 0;
     float pk = 0.f;
     if constexpr (E == 2) {
       pk = dot8_bf16(qraw[0], kraw[t][0], 0.f);
@@ -188,13 +206,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
       for (int e = 0; e < 8; ++e) pk = fmaf(q[e], kx[e], pk);
     }
     float part = pk * pgain[t];
-    if constexpr (HAS_SE) {
-      if constexpr (E == 2) Vec8<T>::load(reinterpret_cast<const T*>(qraw), q);
-      if (lane_ok) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) part = fmaf(q[e], p.scale_embed[jj * D + d0 + e], part);
-      }
-    }
+    if constexpr (HAS_SE) part += sed[t];
     const float tot = group_sum<G>(part);
     s[t] = ok[t] ? fmaf(tot, c, pbias[t]) : -INFINITY;
   }
