@@ -87,19 +87,31 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   // The wave index is uniform: readfirstlane keeps (b, h), the row pointers and the ring's buffer
   // resources in scalar registers (a resource in vector registers costs every load a loop).
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const long long bh = (long long)blockIdx.x * (kBlock / 64) + wave;
-  if (bh >= (long long)p.B * p.H) return;
-  const int b = (int)bh / p.H, h = (int)bh - b * p.H;  // B * H < 2^31 (checked by the ABI)
+  // One round trip for the kernel arguments before the position's: the arguments the prologue
+  // needs pass through one empty asm statement that everything after it depends on, so their
+  // scalar loads go out together and are waited for once (otherwise the compiler waits for B
+  // and H, divides, and only then asks for the pointers).  For the same reason no wave exits
+  // early: waves past the last (b,h) (B * H not a multiple of four) repeat it and store nothing.
+  int nB = p.B, nH = p.H, J = p.taps.J;
+  const long long* posp = p.pos;
+  const void *qp = p.q, *knp = p.k_new, *vnp = p.v_new;
+  const float* pbp = p.pos_bias;
+  asm volatile("" : "+s"(nB), "+s"(nH), "+s"(J) : "s"(posp), "s"(qp), "s"(knp), "s"(vnp), "s"(pbp));
+  const long long nbh = (long long)nB * nH;
+  const long long bh_w = (long long)blockIdx.x * (kBlock / 64) + wave;
+  const bool live = bh_w < nbh;
+  const long long bh = live ? bh_w : nbh - 1;
+  const int b = (int)bh / nH, h = (int)bh - b * nH;  // B * H < 2^31 (checked by the ABI)
   const int r = lane / G, g = lane - r * G;
   const int d0 = g * 8;
   const bool lane_ok = d0 < D;
-  const int J = p.taps.J, S = p.S;
+  const int S = p.S;
   const float c = p.scale;
-  const long long pos = p.pos[b];  // waited for at the validity test below
+  const long long pos = posp[b];  // waited for at the validity test below
   T* outrow = static_cast<T*>(p.out) + bh * D;
-  const T* qrow = static_cast<const T*>(p.q) + bh * D;
-  const T* knew = static_cast<const T*>(p.k_new) + bh * D;
-  const T* vnew = static_cast<const T*>(p.v_new) + bh * D;
+  const T* qrow = static_cast<const T*>(qp) + bh * D;
+  const T* knew = static_cast<const T*>(knp) + bh * D;
+  const T* vnew = static_cast<const T*>(vnp) + bh * D;
 
   // Two memory round trips per step.  Everything that does not depend on the position (query,
   // new key/value row, per-tap bias, gain and scale_embed) is requested before the position is
@@ -119,7 +131,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   for (int t = 0; t < P; ++t) {
     const int j = t * R + r;
     const int jj = j < J ? j : 0;
-    pbias[t] = p.pos_bias[jj * p.H + h];
+    pbias[t] = pbp[jj * nH + h];
     pgain[t] = p.score_gain ? p.score_gain[h * J + jj] : 1.0f;
   }
   float q[8];
@@ -144,8 +156,8 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   }
 
   if (pos < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
-    if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
-    if (lane < G && lane_ok) {
+    if (live && p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
+    if (live && lane < G && lane_ok) {
       float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = __int_as_float(0x7fc00000);
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     }
     return;
   }
-  if (p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos + 1;
+  if (live && p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos + 1;
 
   T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
   T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
@@ -165,7 +177,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   // Slot of tap delta: (pos mod S) - delta, wrapped once (0 < delta < S).  The new row goes
   // into slot pos mod S now: no tap of this step reads that slot.
   const int base = (pos >> 31) == 0 ? (int)pos % S : (int)(pos % S);  // 32-bit when it fits
-  if (r == 0 && lane_ok) {
+  if (live && r == 0 && lane_ok) {
 #pragma unroll
     for (int u = 0; u < C16; ++u) {
       st16(kring + base * D + d0 + 4 * u * (E == 4), knraw[u]);
@@ -236,7 +248,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   const float inv = a / l;
   if constexpr (G == 16) {  // two elements per lane: 4 (lane>>5 & 1) + 2 (lane>>4 & 1) + {0,1}
     const int e0 = 4 * ((lane >> 5) & 1) + 2 * ((lane >> 4) & 1);
-    if (lane_ok) {
+    if (live && lane_ok) {
       if constexpr (E == 2) {
         *reinterpret_cast<unsigned*>(outrow + d0 + e0) =
             f32_to_bf16(acc[0] * inv) | (f32_to_bf16(acc[1] * inv) << 16);
@@ -244,7 +256,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
         *reinterpret_cast<float2*>(outrow + d0 + e0) = make_float2(acc[0] * inv, acc[1] * inv);
       }
     }
-  } else if (G == 8 || (r & 1) == 0) {  // one element per lane (D = 32: both lanes of a pair hold it)
+  } else if (live && (G == 8 || (r & 1) == 0)) {  // one element per lane (D = 32: both lanes of a pair hold it)
     const int e0 = (lane >> 3) & 7;
     if constexpr (E == 2) {
       outrow[d0 + e0] = (T)f32_to_bf16(acc[0] * inv);
