@@ -21,8 +21,11 @@
 // (strides 16 and 32 lanes), across the four waves one LDS exchange; a lane reads every 16th
 // earlier chunk sum.  Every sum runs in a fixed order: results are deterministic.
 //
-// Element types are per tensor (f32, bf16, f16) and uniform per launch, so the type switch at
-// each load is a scalar branch.  As torch computes sigmoid in the gate's dtype, s is rounded
+// Element types are per tensor (f32, bf16, f16) and uniform per launch.  A launch whose tensors
+// are all bf16 runs kernels compiled for that type; any other mix switches at each load on the
+// tensor's type (a scalar branch), which splits the loads into separately waited groups and
+// costs registers (at [8, 2048, 768] bf16: forward 24.5 -> 18.6 us, backward 58.1 -> 40.1 us
+// for the compiled-type kernels).  As torch computes sigmoid in the gate's dtype, s is rounded
 // to that dtype before it is used; all arithmetic is fp32, with 1/(n+1) and the sigmoid's
 // reciprocal from v_rcp_f32 (1 ulp).
 #include "../../include/dsqg.h"
@@ -77,6 +80,11 @@ __device__ __forceinline__ float round_to(int dt, float x) {
 __device__ __forceinline__ float sigmoid_as(int dt, float g) {
   return round_to(dt, __builtin_amdgcn_rcpf(1.0f + __expf(-g)));
 }
+
+// Element type of a launch's tensors: DT when the launch fixes one type for all of them (the
+// type branches then fold away at compile time), else the tensor's own runtime type (DT = -1).
+template <int DT>
+__device__ __forceinline__ int dt_of(int runtime_dt) { return DT >= 0 ? DT : runtime_dt; }
 
 // Lane coordinates: tid = rl * 16 + cgl, so a wave holds 16 channel groups x 4 row lanes.
 struct PoolLane {
@@ -140,6 +148,44 @@ __device__ __forceinline__ void tload(const TensorRows& t, int r, float (&v)[kCp
     v[2] = f16_to_f32(w.y & 0xffffu); v[3] = f16_to_f32(w.y >> 16);
   }
 }
+
+// A lane's RPL rows x kCpl channels kept for a later pass over the rows.  PACK (the tensor is
+// bf16, and so is every value kept): as packed bf16 pairs, half the registers, one VALU
+// instruction to unpack an element.  Otherwise as floats.
+template <int RPL, bool PACK>
+struct RowBuf {
+  float v[RPL][kCpl];
+  // Loads row r into the buffer and returns it in a.
+  __device__ __forceinline__ void load(const TensorRows& t, int r, float (&a)[kCpl]) {
+    tload(t, r, v[r]);
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) a[e] = v[r][e];
+  }
+  __device__ __forceinline__ void set(int r, const float (&a)[kCpl]) {
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) v[r][e] = a[e];
+  }
+  __device__ __forceinline__ float get(int r, int e) const { return v[r][e]; }
+};
+
+template <int RPL>
+struct RowBuf<RPL, true> {
+  uint32_t w[RPL][2];
+  __device__ __forceinline__ void load(const TensorRows& t, int r, float (&a)[kCpl]) {
+    const uint2 u = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(t.r, t.lane, r * t.rstep, 0));
+    w[r][0] = u.x; w[r][1] = u.y;
+#pragma unroll
+    for (int e = 0; e < kCpl; ++e) a[e] = get(r, e);
+  }
+  __device__ __forceinline__ void set(int r, const float (&a)[kCpl]) {  // a: bf16 values
+    w[r][0] = pack2_bf16(a[0], a[1]);
+    w[r][1] = pack2_bf16(a[2], a[3]);
+  }
+  __device__ __forceinline__ float get(int r, int e) const {
+    const uint32_t u = w[r][e >> 1];
+    return __uint_as_float((e & 1) ? (u & 0xffff0000u) : (u << 16));
+  }
+};
 
 // Store channels c..c+3 of row row0 + r (dropped beyond the slice).  Callers skip inactive
 // lanes, whose channels lie past C (inside another row's stride gap).  Stores are at most 8
@@ -247,11 +293,12 @@ struct ChunkCarry {
 };
 
 // ---- Pass 1: chunk sums of x (and, backward, of dout * s / (n+1)). -----------------------
-template <int RPL, bool BWD>
+template <int RPL, bool BWD, int DT>
 __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
+  const int gdt = dt_of<DT>(p.gdt);
+  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, dt_of<DT>(p.xdt), p, q);
   float ax[kCpl], ap[kCpl];
 #pragma unroll
   for (int e = 0; e < kCpl; ++e) ax[e] = ap[e] = 0.f;
@@ -263,8 +310,8 @@ __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
     for (int e = 0; e < kCpl; ++e) ax[e] += v[e];
   }
   if constexpr (BWD) {
-    const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
-    const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
+    const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, gdt, p, q);
+    const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, dt_of<DT>(p.ydt), p, q);
 #pragma unroll
     for (int r = 0; r < RPL; ++r) {
       float gv[kCpl], yv[kCpl];
@@ -272,7 +319,7 @@ __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
       tload(ty, r, yv);   // zero beyond N, so those rows add nothing
       const float inv = __builtin_amdgcn_rcpf((float)(q.row0 + r + 1));
 #pragma unroll
-      for (int e = 0; e < kCpl; ++e) ap[e] += yv[e] * sigmoid_as(p.gdt, gv[e]) * inv;
+      for (int e = 0; e < kCpl; ++e) ap[e] += yv[e] * sigmoid_as(gdt, gv[e]) * inv;
     }
   }
   rl_total(ax, sW);
@@ -285,12 +332,13 @@ __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
 }
 
 // ---- Pass 2, forward: out = s * (carry + running sum) / (n+1). ----------------------------
-template <int RPL>
+template <int RPL, int DT>
 __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
-  const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
+  const int gdt = dt_of<DT>(p.gdt);
+  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, dt_of<DT>(p.xdt), p, q);
+  const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, gdt, p, q);
   ChunkCarry cc;
   cc.begin(p.px, p, q, q.rl, q.chunk);
   float x[RPL][kCpl], s[RPL][kCpl];
@@ -304,7 +352,7 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
     tload(tg, r, gv);
 #pragma unroll
     for (int e = 0; e < kCpl; ++e) {
-      s[r][e] = sigmoid_as(p.gdt, gv[e]);
+      s[r][e] = sigmoid_as(gdt, gv[e]);
       run[e] += x[r][e];
     }
   }
@@ -314,7 +362,7 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
   rl_exclusive_scan<false>(run, sW);
 #pragma unroll
   for (int e = 0; e < kCpl; ++e) run[e] += carry[e];
-  const TensorRows to = rows_of(p.out, p.os_b, p.os_n, p.odt, p, q);
+  const TensorRows to = rows_of(p.out, p.os_b, p.os_n, dt_of<DT>(p.odt), p, q);
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     const int n = q.row0 + r;
@@ -330,34 +378,37 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
 }
 
 // ---- Pass 2, backward. ----------------------------------------------------------------------
-template <int RPL>
+template <int RPL, int DT>
 __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
   const PoolLane q = pool_lane<RPL>(p);
-  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, p.xdt, p, q);
-  const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, p.gdt, p, q);
-  const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, p.ydt, p, q);
+  const int xdt = dt_of<DT>(p.xdt), gdt = dt_of<DT>(p.gdt);
+  const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, xdt, p, q);
+  const TensorRows tg = rows_of(p.g, p.gs_b, p.gs_n, gdt, p, q);
+  const TensorRows ty = rows_of(p.dy, p.ys_b, p.ys_n, dt_of<DT>(p.ydt), p, q);
   ChunkCarry ccx, ccp;
   ccx.begin(p.px, p, q, q.rl, q.chunk);
   ccp.begin(p.pp, p, q, q.chunk + 1 + q.rl, p.nchunks);
-  float x[RPL][kCpl], s[RPL][kCpl], y[RPL][kCpl];
+  constexpr bool kPack = DT == DSQG_BF16;
+  RowBuf<RPL, kPack> x, s, y;
   float runx[kCpl], runp[kCpl];
 #pragma unroll
   for (int e = 0; e < kCpl; ++e) runx[e] = runp[e] = 0.f;
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     const int n = q.row0 + r;
-    float gv[kCpl];
-    tload(tx, r, x[r]);
+    float xv[kCpl], gv[kCpl], yv[kCpl], sv[kCpl];
+    x.load(tx, r, xv);
     tload(tg, r, gv);
-    tload(ty, r, y[r]);   // zero beyond N: those rows add nothing below
+    y.load(ty, r, yv);   // zero beyond N: those rows add nothing below
 #pragma unroll
-    for (int e = 0; e < kCpl; ++e) s[r][e] = sigmoid_as(p.gdt, gv[e]);
+    for (int e = 0; e < kCpl; ++e) sv[e] = sigmoid_as(gdt, gv[e]);
+    s.set(r, sv);
     const float inv = __builtin_amdgcn_rcpf((float)(n + 1));
 #pragma unroll
     for (int e = 0; e < kCpl; ++e) {
-      runx[e] += x[r][e];
-      runp[e] += y[r][e] * s[r][e] * inv;   // dout * s / (n+1), recomputed the same way below
+      runx[e] += xv[e];
+      runp[e] += yv[e] * sv[e] * inv;   // dout * s / (n+1), recomputed the same way below
     }
   }
   float cx[kCpl], cp[kCpl];
@@ -372,8 +423,8 @@ __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) 
     runx[e] += cx[e];
     runp[e] += cp[e];
   }
-  const TensorRows tdg = rows_of(p.dg ? p.dg : p.x, p.dgs_b, p.dgs_n, p.gdt, p, q);
-  const TensorRows tdx = rows_of(p.dx ? p.dx : p.x, p.dxs_b, p.dxs_n, p.xdt, p, q);
+  const TensorRows tdg = rows_of(p.dg ? p.dg : p.x, p.dgs_b, p.dgs_n, gdt, p, q);
+  const TensorRows tdx = rows_of(p.dx ? p.dx : p.x, p.dxs_b, p.dxs_n, xdt, p, q);
   // dgate_pre on the way down the rows (prefix sums of x) ...
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
@@ -382,8 +433,9 @@ __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) 
     float o[kCpl];
 #pragma unroll
     for (int e = 0; e < kCpl; ++e) {
-      runx[e] += x[r][e];
-      o[e] = y[r][e] * (runx[e] * inv) * (s[r][e] * (1.0f - s[r][e]));
+      const float se = s.get(r, e);
+      runx[e] += x.get(r, e);
+      o[e] = y.get(r, e) * (runx[e] * inv) * (se * (1.0f - se));
     }
     if (p.dg && q.active) tstore(tdg, r, o);
   }
@@ -395,7 +447,7 @@ __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) 
     float o[kCpl];
 #pragma unroll
     for (int e = 0; e < kCpl; ++e) {
-      runp[e] += y[r][e] * s[r][e] * inv;
+      runp[e] += y.get(r, e) * s.get(r, e) * inv;
       o[e] = runp[e];
     }
     if (p.dx && q.active) tstore(tdx, r, o);
@@ -410,8 +462,8 @@ struct PoolPlan {
 };
 
 // 64 channels per workgroup; rows per lane: the most (4, 2, 1) that still gives at least 1024
-// workgroups.  (The backward scan at 4 rows is held to 128 VGPRs, four workgroups per CU, at
-// the cost of a few spilled registers: 60 us instead of 65 at [8, 2048, 768] bf16.)
+// workgroups.  (The backward scan at 4 rows is held to 128 VGPRs, four workgroups per CU: the
+// bf16 kernel fits in 119 with its kept rows packed, the runtime-type one spills a few.)
 PoolPlan pool_plan(int B, int N, int C) {
   PoolPlan pl;
   pl.ctiles = (C + kPoolCh - 1) / kPoolCh;
@@ -454,16 +506,31 @@ size_t pool_workspace(int B, int N, int C, bool bwd) {
   return bwd ? 2 * one : one;
 }
 
-template <int RPL>
+template <int RPL, int DT>
 void launch_pool_fwd(const PoolParams& p, unsigned grid, hipStream_t st) {
-  hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, false>), dim3(grid), dim3(kBlock), 0, st, p);
-  hipLaunchKernelGGL((pool_fwd_scan_kernel<RPL>), dim3(grid), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, false, DT>), dim3(grid), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((pool_fwd_scan_kernel<RPL, DT>), dim3(grid), dim3(kBlock), 0, st, p);
 }
 
-template <int RPL>
+template <int RPL, int DT>
 void launch_pool_bwd(const PoolParams& p, unsigned grid, hipStream_t st) {
-  hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, true>), dim3(grid), dim3(kBlock), 0, st, p);
-  hipLaunchKernelGGL((pool_bwd_scan_kernel<RPL>), dim3(grid), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((pool_chunk_sum_kernel<RPL, true, DT>), dim3(grid), dim3(kBlock), 0, st, p);
+  hipLaunchKernelGGL((pool_bwd_scan_kernel<RPL, DT>), dim3(grid), dim3(kBlock), 0, st, p);
+}
+
+// All-bf16 launches (the modules' case) run kernels compiled for bf16; any other mix of types
+// runs the kernels that switch on each tensor's runtime type.
+template <int RPL>
+void launch_pool(const PoolParams& p, bool bwd, unsigned grid, hipStream_t st) {
+  const bool all_bf16 = p.xdt == DSQG_BF16 && p.gdt == DSQG_BF16 && p.ydt == DSQG_BF16 &&
+                        p.odt == DSQG_BF16;
+  if (bwd) {
+    if (all_bf16) launch_pool_bwd<RPL, DSQG_BF16>(p, grid, st);
+    else launch_pool_bwd<RPL, -1>(p, grid, st);
+  } else {
+    if (all_bf16) launch_pool_fwd<RPL, DSQG_BF16>(p, grid, st);
+    else launch_pool_fwd<RPL, -1>(p, grid, st);
+  }
 }
 
 int run_pool(PoolParams& p, bool bwd, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -479,15 +546,9 @@ int run_pool(PoolParams& p, bool bwd, void* ws, size_t ws_bytes, hipStream_t st)
   p.ctiles = pl.ctiles;
   p.L = pl.L;
   const unsigned grid = (unsigned)pl.grid;
-  if (bwd) {
-    if (pl.rpl == 4) launch_pool_bwd<4>(p, grid, st);
-    else if (pl.rpl == 2) launch_pool_bwd<2>(p, grid, st);
-    else launch_pool_bwd<1>(p, grid, st);
-  } else {
-    if (pl.rpl == 4) launch_pool_fwd<4>(p, grid, st);
-    else if (pl.rpl == 2) launch_pool_fwd<2>(p, grid, st);
-    else launch_pool_fwd<1>(p, grid, st);
-  }
+  if (pl.rpl == 4) launch_pool<4>(p, bwd, grid, st);
+  else if (pl.rpl == 2) launch_pool<2>(p, bwd, grid, st);
+  else launch_pool<1>(p, bwd, grid, st);
   return hipGetLastError() == hipSuccess ? DSQG_OK : DSQG_EHIP;
 }
 
