@@ -61,11 +61,13 @@ def _inputs(B, N, C, xdt, gdt, seed):
 
 
 @pytest.mark.parametrize("shape", [(1, 1, 8), (2, 37, 24), (3, 300, 256), (2, 2048, 512),
-                                   (1, 5000, 64), (4, 1100, 1032)])
+                                   (1, 5000, 64), (4, 1100, 1032), (4, 4100, 520)])
 @pytest.mark.parametrize("xdt,gdt", [(F32, F32), (F32, F16), (BF16, BF16), (F16, F16)])
 def test_pool_gate_matches_oracle(gpu_device, shape, xdt, gdt):
-    """Forward and both gradients through the autograd op, ragged N and C included (the last
-    shape: N and C off every power of two, 17 workgroup columns of 64 channels)."""
+    """Forward and both gradients through the autograd op, ragged N and C included ((4, 1100,
+    1032): N and C off every power of two, 17 workgroup columns of 64 channels; (4, 4100, 520):
+    the forward's 8-rows-per-lane plan, 128-row chunks with a ragged last chunk and a last
+    column of 8 channels)."""
     B, N, C = shape
     _say(f"shape={shape} x={xdt} gate={gdt}")
     x, gp, dy = _inputs(B, N, C, xdt, gdt, seed=B * 7919 + N)
