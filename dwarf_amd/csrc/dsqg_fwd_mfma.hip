@@ -77,6 +77,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   const int n0 = tile * QT;
   const float c2 = p.scale * kLog2e;
   const int qsn = (int)p.qs.n, ksn = (int)p.ks.n, vsn = (int)p.vs.n;
+  // The IF gain is requested with the first loads: read after the softmax, it cost every wave a
+  // fresh memory round trip, and its wait also held the dense P V for the long-range V prefetch.
+  const float if_a = p.if_gain ? p.if_gain[h] : 1.0f;
 
   const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
   const __amdgpu_buffer_rsrc_t rK = slice_rsrc(static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h, p.ks.n, N, D);
@@ -295,8 +298,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   lsum = col_sum(lsum);
   const long long rowbase = ((long long)b * p.H + h) * N;
   if (row_ok && g == 0 && p.lse) p.lse[rowbase + n] = (mx + __log2f(lsum)) * 0.6931471805599453f;
-  const float a = p.if_gain ? p.if_gain[h] : 1.0f;
-  const float inv = row_ok ? a / lsum : 0.f;
+  const float inv = row_ok ? if_a / lsum : 0.f;
 
   // ---- Dense P V: O^T = V^T P^T. ----
   f32x4_t accO[DB];
