@@ -116,6 +116,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     wq[u] = bload16(rQ, m0 * qsn + opaque(cv ? (ci / CPS) * qsn + (ci % CPS) * 8 : kNoElem));
     wo[u] = bload16(rO, m0 * dosn + opaque(cv ? (ci / CPS) * dosn + (ci % CPS) * 8 : kNoElem));
   }
+  // Per-tap bias and gain (J <= kMaxTaps < kBlock: one per thread), requested with the window
+  // rows, so that storing them below waits for those rows only (requested after every load,
+  // they made wave 0 wait for all of its loads before the first barrier).
+  const int jc = tid < J ? tid : J - 1;
+  const float bias_ld = p.pos_bias[jc * p.H + h];
+  const float gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
   bf16x8_t kB[KS], vB[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
@@ -149,11 +155,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     dpS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
   };
 
-  for (int j = tid; j < J; j += kBlock) {
-    const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
-    sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
-    sGain2[j] = gj * c2;
-    sGainC[j] = gj * c;
+  if (tid < J) {
+    sBias2[tid] = bias_ld * kLog2e;
+    sGain2[tid] = gain_ld * c2;
+    sGainC[tid] = gain_ld * c;
   }
   if constexpr (HAS_SE) seR.template store<RV>(sSE, nullptr, tid);
 #pragma unroll

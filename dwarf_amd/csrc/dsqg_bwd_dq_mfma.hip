@@ -117,14 +117,23 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
   }
 
-  for (int j = tid; j < J; j += kBlock) {
-    const float gj = p.score_gain ? p.score_gain[h * J + j] : 1.0f;
-    sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
-    sGain[j] = gj;
-  }
+  // Per-tap bias and gain (J <= kMaxTaps < kBlock: one per thread).  With scale_embed they are
+  // staged here, with the scale_embed rows, all requested before the one wait: held in registers
+  // across the tile's loads instead, they cost that kernel three spilled registers and 1.3 us.
+  // Without it they are requested after the window rows and stored just before the first
+  // barrier, which waits for those rows anyway.  (Stored before any tile load was issued, their
+  // wait held back every load of the workgroup by a memory round trip.)
+  const int jc = tid < J ? tid : J - 1;
+  [[maybe_unused]] float bias_ld = 0.f, gain_ld = 1.f;
   if constexpr (HAS_SE) {
+    bias_ld = p.pos_bias[jc * p.H + h];
+    gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
     SeRows<D> seR;
     seR.load(p.scale_embed, J, tid);
+    if (tid < J) {
+      sBias2[tid] = bias_ld * kLog2e;
+      sGain[tid] = gain_ld;
+    }
     seR.template store<RV>(sSE, sSElo, tid);
   }
 
@@ -171,6 +180,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
       wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
       wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
     }
+    if constexpr (!HAS_SE) {
+      bias_ld = p.pos_bias[jc * p.H + h];
+      gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
+    }
     bf16x8_t qB[KS], oB[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -184,7 +197,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
       qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
       oR[u] = bload16(rO, n0w * dosn + olaneR[u]);
     }
-    const float lse2 = row_ok ? p.lse[rowbase + n] * kLog2e : 0.f;
+    // Unconditional (a row past N reads row N - 1 and is masked below): a load under the row
+    // test was waited for inside the branch, before the long-range loads could be issued.
+    const float lse_ld = p.lse[rowbase + (row_ok ? n : N - 1)];
     // Long-range K/V rows n0w - delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
     uint4 kS[PF][CHW], vS[PF][CHW];
 #pragma unroll
@@ -197,6 +212,11 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
           vS[t][u] = bload16(rV, m0 * vsn + vlaneR[u]);
         }
       }
+    }
+
+    if (!HAS_SE && tid < J) {
+      sBias2[tid] = bias_ld * kLog2e;
+      sGain[tid] = gain_ld;
     }
 
     __syncthreads();  // previous tile's readers of sK / tables are done
@@ -250,6 +270,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     float al[12], uu[12];
     float dlane = 0.f, wlane = 0.f;
     const int dl0 = 32 - 4 * g + i;
+    const float lse2 = row_ok ? lse_ld * kLog2e : 0.f;
 #pragma unroll
     for (int kk = 0; kk < 3; ++kk) {
 #pragma unroll
