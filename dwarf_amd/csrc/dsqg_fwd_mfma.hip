@@ -106,8 +106,19 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
     klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
   }
+  // Per-tap bias and gain (J <= kMaxTaps < kBlock: one per thread), stored to LDS below after a
+  // wait that must cover as few loads as possible: with scale_embed they go first, with the
+  // scale_embed rows (the T table needs them all), without it after the window rows (the first
+  // barrier waits for those anyway).  Requested after every other load, they made wave 0 wait
+  // for its long-range key gathers before the first barrier.
+  const int jc = tid < J ? tid : J - 1;
+  float bias_ld = 0.f, gain_ld = 1.f;
   SeRows<D> seR;
-  if constexpr (HAS_SE) seR.load(p.scale_embed, J, tid);
+  if constexpr (HAS_SE) {
+    bias_ld = p.pos_bias[jc * p.H + h];
+    gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
+    seR.load(p.scale_embed, J, tid);
+  }
   bf16x8_t qB[KS];
   if constexpr (HAS_SE) {
     const int qlane = opaque(i * qsn + 8 * g);
@@ -127,6 +138,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
     wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
   }
+  if constexpr (!HAS_SE) {
+    bias_ld = p.pos_bias[jc * p.H + h];
+    gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
+  }
   // The long-range key rows n0w - delta + 0..15 in the row-chunk layout, in two halves (the
   // second after the dense band has consumed its registers) to bound the register peak.
   constexpr int NH = (NSM + 1) / 2;
@@ -139,9 +154,9 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
       for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
     }
   }
-  for (int j = tid; j < J; j += kBlock) {
-    sBias2[j] = p.pos_bias[j * p.H + h] * kLog2e;
-    sGain2[j] = (p.score_gain ? p.score_gain[h * J + j] : 1.0f) * c2;
+  if (tid < J) {
+    sBias2[tid] = bias_ld * kLog2e;
+    sGain2[tid] = gain_ld * c2;
   }
   float* sTw = reinterpret_cast<float*>(sVs[w]);  // T table until the long-range P V
   if constexpr (HAS_SE) {
