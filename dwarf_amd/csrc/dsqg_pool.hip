@@ -86,6 +86,16 @@ __device__ __forceinline__ float sigmoid_as(int dt, float g) {
 template <int DT>
 __device__ __forceinline__ int dt_of(int runtime_dt) { return DT >= 0 ? DT : runtime_dt; }
 
+// The kernel arguments a prologue needs, requested in one round trip: they pass through one
+// empty asm statement that everything after it depends on (otherwise the compiler waits for
+// the grid constants, divides, and only then asks for the pointers, strides and sizes: three
+// dependent scalar round trips before the first row load).
+__device__ __forceinline__ void pool_args_at_once(PoolParams& p) {
+  asm volatile("" : "+s"(p.ctiles), "+s"(p.nchunks), "+s"(p.N), "+s"(p.C), "+s"(p.L)
+               : "s"(p.x), "s"(p.g), "s"(p.dy), "s"(p.px), "s"(p.pp), "s"(p.xs_b), "s"(p.xs_n),
+                 "s"(p.gs_b), "s"(p.gs_n), "s"(p.ys_b), "s"(p.ys_n));
+}
+
 // Lane coordinates: tid = rl * 16 + cgl, so a wave holds 16 channel groups x 4 row lanes.
 struct PoolLane {
   int b, chunk, cgl, rl, c;  // c: first channel of this lane; active iff c < C
@@ -296,6 +306,7 @@ struct ChunkCarry {
 template <int RPL, bool BWD, int DT>
 __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
+  pool_args_at_once(p);
   const PoolLane q = pool_lane<RPL>(p);
   const int gdt = dt_of<DT>(p.gdt);
   const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, dt_of<DT>(p.xdt), p, q);
@@ -335,6 +346,7 @@ __global__ __launch_bounds__(kBlock) void pool_chunk_sum_kernel(PoolParams p) {
 template <int RPL, int DT>
 __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
+  pool_args_at_once(p);
   const PoolLane q = pool_lane<RPL>(p);
   const int gdt = dt_of<DT>(p.gdt);
   const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, dt_of<DT>(p.xdt), p, q);
@@ -381,6 +393,7 @@ __global__ __launch_bounds__(kBlock) void pool_fwd_scan_kernel(PoolParams p) {
 template <int RPL, int DT>
 __global__ __launch_bounds__(kBlock, 4) void pool_bwd_scan_kernel(PoolParams p) {
   __shared__ float sW[4 * 64];
+  pool_args_at_once(p);
   const PoolLane q = pool_lane<RPL>(p);
   const int xdt = dt_of<DT>(p.xdt), gdt = dt_of<DT>(p.gdt);
   const TensorRows tx = rows_of(p.x, p.xs_b, p.xs_n, xdt, p, q);
