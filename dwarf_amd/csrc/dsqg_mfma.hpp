@@ -110,10 +110,12 @@ __device__ __forceinline__ int rc_lane(int l, int u, int rs) {
 // Buffer resource over one (b,h) slice of a [B,H,N,D] bf16 operand: rows [0, N) of row stride rs
 // elements.  Raw buffer loads range-check each access against the slice size, so a row below 0
 // (negative 32-bit offset, i.e. a huge unsigned one) or at/after N reads as zeros -- the masked
-// taps cost no branch.  The caller guarantees (N + max offset) * rs * 2 < 2^31 and rs >= D.
+// taps cost no branch.  The caller guarantees (N + max offset) * rs * 2 < 2^31 and rs >= D, and
+// N >= 1 (no kernel is launched for N = 0): the extent is then computed without a branch (one
+// branch per operand split the prologue's kernel-argument loads into separately waited groups).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t slice_rsrc(const bf16_t* base, long long rs,
                                                              int N, int D) {
-  const int bytes = N > 0 ? (int)(((long long)(N - 1) * rs + D) * 2) : 0;
+  const int bytes = (int)(((long long)(N - 1) * rs + D) * 2);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), (short)0, bytes,
                                            0x00020000);
 }
