@@ -70,6 +70,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     reduce_params_wave(p.red, ((int)blockIdx.x - kv_blocks) * (kBlock / 64) + __builtin_amdgcn_readfirstlane(tid >> 6), tid & 63);
     return;
   }
+  // The kernel arguments of the prologue in one round trip: sizes and input strides pass through
+  // an empty asm statement that the code after it depends on, the input pointers are its
+  // operands, so all are requested before it and waited for once (otherwise the grid constants
+  // come first, the block-number divisions wait for them, and each later group of arguments
+  // costs another dependent round trip).
+  asm volatile("" : "+s"(p.H), "+s"(p.N), "+s"(p.n_tiles_kv), "+s"(p.taps.J), "+s"(p.taps.W),
+               "+s"(p.qs.b), "+s"(p.qs.h), "+s"(p.qs.n), "+s"(p.ks.b), "+s"(p.ks.h), "+s"(p.ks.n),
+               "+s"(p.vs.b), "+s"(p.vs.h), "+s"(p.vs.n), "+s"(p.dos.b), "+s"(p.dos.h), "+s"(p.dos.n)
+               : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.dout), "s"(p.lse), "s"(p.dpre), "s"(p.pos_bias),
+                 "s"(p.if_gain));
   const int lb = xcd_logical_block(blockIdx.x, kv_blocks);
   const int bh = lb / p.n_tiles_kv, tile = lb - bh * p.n_tiles_kv;
   const int b = bh / p.H, h = bh - b * p.H;

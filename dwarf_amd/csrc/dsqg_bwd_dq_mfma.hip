@@ -87,7 +87,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   __shared__ __align__(16) float sPair[4][16][2];
 
   const int tid = threadIdx.x;
-  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  // The kernel arguments of the prologue in one round trip: sizes and input strides pass through
+  // an empty asm statement that the code after it depends on, the input pointers are its
+  // operands, so all are requested before it and waited for once (otherwise the grid constants
+  // come first, the block-number divisions wait for them, and each later group of arguments
+  // costs another dependent round trip).
+  int nblk = (int)gridDim.x;
+  asm volatile("" : "+s"(nblk), "+s"(p.H), "+s"(p.N), "+s"(p.n_chunks), "+s"(p.taps.J), "+s"(p.taps.W),
+               "+s"(p.qs.b), "+s"(p.qs.h), "+s"(p.qs.n), "+s"(p.ks.b), "+s"(p.ks.h), "+s"(p.ks.n),
+               "+s"(p.vs.b), "+s"(p.vs.h), "+s"(p.vs.n), "+s"(p.dos.b), "+s"(p.dos.h), "+s"(p.dos.n)
+               : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.dout), "s"(p.lse), "s"(p.pos_bias), "s"(p.if_gain));
+  const int lb = xcd_logical_block(blockIdx.x, nblk);
   const int bh = lb / p.n_chunks, chunk = lb - bh * p.n_chunks;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;

@@ -69,7 +69,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
 
   const int tid = threadIdx.x;
-  const int lb = xcd_logical_block(blockIdx.x, gridDim.x);
+  // The kernel arguments of the prologue in one round trip: sizes and input strides pass through
+  // an empty asm statement that the code after it depends on, the input pointers are its
+  // operands, so all are requested before it and waited for once (otherwise the grid constants
+  // come first, the block-number divisions wait for them, and each later group of arguments
+  // costs another dependent round trip).
+  int nblk = (int)gridDim.x;
+  asm volatile("" : "+s"(nblk), "+s"(p.H), "+s"(p.N), "+s"(p.n_tiles), "+s"(p.taps.J), "+s"(p.taps.W),
+               "+s"(p.qs.b), "+s"(p.qs.h), "+s"(p.qs.n), "+s"(p.ks.b), "+s"(p.ks.h), "+s"(p.ks.n),
+               "+s"(p.vs.b), "+s"(p.vs.h), "+s"(p.vs.n)
+               : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.pos_bias), "s"(p.if_gain));
+  const int lb = xcd_logical_block(blockIdx.x, nblk);
   const int bh = lb / p.n_tiles, tile = lb - bh * p.n_tiles;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;
