@@ -548,75 +548,6 @@ def profile_pool(args, dev):
     return 0
 
 
-def run_probes(dev, reps=20):
-    """Memory-system probes (bench_probes.hip, dwarf_amd/libdsqg_probes.so): 2 KB block-gather
-    bandwidth from an L2-resident, an L2-exceeding and an HBM-sized region, and the config-2
-    forward's memory skeleton (window, query and output rows; with and without the 11 long-range
-    K/V gathers; tiles in the kernels' XCD-aware order, and the gathers once more without it),
-    timed with HIP events on the current stream.  Prints one JSON line."""
-    import ctypes
-    import torch
-    from dwarf_amd.build import PROBE_LIB_PATH
-    from dwarf_amd.workloads import WORKLOADS
-    if not PROBE_LIB_PATH.exists():
-        print(f"bench.py: {PROBE_LIB_PATH} is not built (python -m dwarf_amd.build)", file=sys.stderr)
-        return 1
-    lib = ctypes.CDLL(str(PROBE_LIB_PATH))
-    vp, i64, ci = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int
-    lib.dsqg_probe_gather.argtypes = [vp, i64, ci, ci, ci, vp, vp]
-    lib.dsqg_probe_fwd_skeleton.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp]
-    stream = torch.cuda.current_stream(dev)
-
-    def timed(fn, n=reps):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize(dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1000.0 / n  # us per launch
-
-    def check(rc, name):
-        if rc != 0:
-            raise RuntimeError(f"{name} returned {rc}")
-
-    res = {"probes": "bench_probes.hip", "gather_2KB_blocks": {}}
-    src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
-    sink = torch.zeros(16, dtype=torch.int32, device=dev)
-    blocks, iters = 2048, 256  # 8 waves per CU, 256 blocks of 2 KB per wave
-    for label, region in (("l2_2MiB", 2 << 20), ("beyond_l2_8MiB", 8 << 20), ("hbm_1GiB", (1 << 30) - 2048)):
-        us = timed(lambda: check(lib.dsqg_probe_gather(src.data_ptr(), region, 4, blocks, iters,
-                                                      sink.data_ptr(), stream.cuda_stream), "gather"), 5)
-        nbytes = blocks * 4 * iters * 2048
-        res["gather_2KB_blocks"][label] = {"us": round(us, 1), "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
-        print(f"[bench] probe gather {label}: {nbytes / (us * 1e-6) / 1e9:.0f} GB/s", file=sys.stderr, flush=True)
-    del src
-    w = WORKLOADS[2]
-    BH, N = w.B * w.H, w.N
-    sets = [[torch.randn(BH, N, 64, device=dev).to(torch.bfloat16) for _ in range(4)] for _ in range(3)]
-    it = [0]
-
-    def skel(g):
-        q, k, v, o = sets[it[0] % 3]
-        it[0] += 1
-        check(lib.dsqg_probe_fwd_skeleton(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), BH, N,
-                                          g, stream.cuda_stream), "fwd_skeleton")
-    fwd_bytes = 4 * BH * N * 64 * 2
-    res["fwd_skeleton_config2"] = {}
-    for label, g in (("window_q_out", 2), ("window_q_out_11_gathers", 3),
-                     ("window_q_out_11_gathers_no_xcd_order", 1)):
-        us = timed(lambda: skel(g))
-        res["fwd_skeleton_config2"][label] = {"us": round(us, 2),
-                                              "GBs_on_fwd_algorithmic_bytes": round(fwd_bytes / (us * 1e-6) / 1e9, 1)}
-        print(f"[bench] probe fwd skeleton {label}: {us:.2f} us", file=sys.stderr, flush=True)
-    res["fwd_skeleton_config2"]["long_range_gather_bytes"] = 11 * 2 * BH * N * 128
-    print(json.dumps(res), flush=True)
-    return 0
-
-
 def make_sets(w, dev, n, scale_embed=False, if_gain=False):
     """`n` input sets of workload w (seeds w.seed + 100 i), each with its launch objects.
     scale_embed / if_gain add the reference module's parameters (se ~ 0.05 N(0,1),
@@ -731,8 +662,6 @@ def main(argv=None):
     ap.add_argument("--profile-reps", type=int, default=5)
     ap.add_argument("--profile-se", action="store_true",
                     help="with --profile-kernel: the scale_embed leg's inputs (scale_embed, if_gain)")
-    ap.add_argument("--probes", action="store_true",
-                    help="run the memory-system probes (bench_probes.hip) and exit with their JSON line")
     ap.add_argument("--copy-mib", type=int, default=256)
     ap.add_argument("--decode-sweep", action="store_true",
                     help="time the decode step (8 ring pairs) at batch 32..512 and a trivial "
@@ -764,8 +693,6 @@ def main(argv=None):
 
     if args.profile_kernel:
         return profile_mode(args, w, dev)
-    if args.probes:
-        return run_probes(dev)
     if args.decode_sweep:
         return decode_sweep(dev, args.decode_steps)
     if args.table_sweep:

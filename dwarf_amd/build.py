@@ -24,10 +24,6 @@ INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libdsqg_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 OBJ_DIR = PKG_DIR / "_build"
-# bench.py's memory-system probes (bench_probes.hip beside bench.py): a library of their own,
-# not linked into the product.
-PROBE_SRC = PKG_DIR.parent / "bench_probes.hip"
-PROBE_LIB_PATH = PKG_DIR / "libdsqg_probes.so"
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -87,23 +83,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     os.replace(tmp, LIB_PATH)
     if verbose:
         print(f"[dwarf_amd.build] linked {LIB_PATH}", flush=True)
-    if PROBE_SRC.exists():
-        build_probes(hipcc, verbose)
     return LIB_PATH
-
-
-def build_probes(hipcc: str | None = None, verbose: bool = True) -> Path:
-    """Compile bench_probes.hip into dwarf_amd/libdsqg_probes.so (used by bench.py --probes)."""
-    hipcc = hipcc or hipcc_path()
-    tmp = PROBE_LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc, *HIPCC_FLAGS, "-shared", "-o", str(tmp), str(PROBE_SRC)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, PROBE_LIB_PATH)
-    if verbose:
-        print(f"[dwarf_amd.build] linked {PROBE_LIB_PATH}", flush=True)
-    return PROBE_LIB_PATH
 
 
 def main(argv=None) -> int:

@@ -181,7 +181,11 @@ int dsqg_bwd_params(const dsqg_bwd_args* args, dsqg_stream_t stream);
  * reference.  For callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  args->workspace and workspace_bytes
  * are ignored; the workspace is a static scratch array of DSQG_NOALLOC_SCRATCH_BYTES on each
- * device, whose address is looked up once per device on the first call there.  A call whose
+ * device.  That array is part of the library's code object, so it takes its 64 MiB of device
+ * memory on every device where the library is loaded, whether or not this entry point is ever
+ * called.  Its address is looked up once per device on the first call there (hipGetSymbolAddress):
+ * make that first call outside stream capture (one eager call), later calls may be captured
+ * into a HIP graph (the call issues kernel launches only, no memset and no allocation).  A call whose
  * workspace (dsqg_bwd_workspace_size) exceeds it returns DSQG_ETOOLARGE before any HIP call.
  * Same kernels, outputs and stream rules as dsqg_bwd; calls that overlap on one device (other
  * streams, other threads) share the scratch and race, so serialise them. */

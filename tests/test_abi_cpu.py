@@ -38,24 +38,6 @@ def test_exports_every_declared_symbol(lib):
     assert lib.dsqg_abi_version() == _lib.ABI_VERSION
 
 
-def test_probe_library_is_separate_and_rejects_bad_arguments(lib):
-    """bench.py's memory-system probes live in a library of their own (not in the product), load
-    without a GPU and refuse arguments outside their documented ranges before any launch."""
-    from dwarf_amd.build import PROBE_LIB_PATH, build_probes
-    if not PROBE_LIB_PATH.exists():
-        build_probes(verbose=False)
-    probes = ctypes.CDLL(str(PROBE_LIB_PATH))
-    vp, i64, ci = ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int
-    probes.dsqg_probe_gather.argtypes = [vp, i64, ci, ci, ci, vp, vp]
-    probes.dsqg_probe_fwd_skeleton.argtypes = [vp, vp, vp, vp, ci, ci, ci, vp]
-    fake = ctypes.c_void_p(0x1000)
-    assert probes.dsqg_probe_gather(fake, 3000, 4, 8, 16, fake, None) == -1      # not 2 KB blocks
-    assert probes.dsqg_probe_gather(fake, 1 << 21, 3, 8, 16, fake, None) == -1   # pf not 1/2/4/8
-    assert probes.dsqg_probe_gather(None, 1 << 21, 4, 8, 16, fake, None) == -1
-    assert probes.dsqg_probe_fwd_skeleton(fake, fake, fake, fake, 4, 100, 3, None) == -1  # N % 64
-    assert not hasattr(lib, "dsqg_probe_gather")
-
-
 def test_ctypes_layout_matches_c(tmp_path):
     from dwarf_amd import _lib
     probes = {
@@ -277,3 +259,35 @@ def test_pool_gate_rejects_bad_arguments(lib):
     assert bcall(b) == E
     b.dx = None; b.dgate_pre = None                       # nothing requested: no launch
     assert bcall(b) == _lib.DSQG_OK
+
+
+def test_bf16_row_span_limit(lib):
+    """bf16 kernels address each (b,h) slice with 32-bit byte offsets: a call is taken while
+    (N + max offset + 64) * (largest row stride) * 2 < 2^31 and refused with DSQG_EUNSUPPORTED
+    past it.  At the headline model width (E 768, heads of 64 read as views of a packed qkv
+    projection, row stride 3 * 768) that is N <= 464,433 with the 44-offset table; checked here
+    through the workspace query and the forward's validation, neither of which launches."""
+    from dwarf_amd import _lib
+    rs, H, D = 3 * 768, 12, 64
+    offs = list(range(33)) + [48, 64, 96, 128, 192, 256, 384, 512, 768, 1024, 1536]
+    n_max = (2 ** 31 - 1) // (2 * rs) - 1536 - 64
+    assert (n_max + 1600) * rs * 2 < 2 ** 31 <= (n_max + 1601) * rs * 2
+    for N, want in ((n_max, _lib.DSQG_OK), (n_max + 1, _lib.DSQG_EUNSUPPORTED)):
+        st = (ctypes.c_int64 * 4)(N * rs, D, rs, 1)
+        b = _lib.BwdArgs()
+        b.shape = _lib.make_shape(_lib.DSQG_BF16, 1, H, N, D, offs)
+        for name in ("q", "k", "v", "dout", "dq", "dk", "dv"):
+            setattr(b, name, 0x10000)
+            setattr(b, name + "_stride", st)
+        b.lse = b.pos_bias = b.dpos_bias = 0x10000
+        n = ctypes.c_size_t(0)
+        assert lib.dsqg_bwd_workspace_size(ctypes.byref(b), ctypes.byref(n)) == want, N
+    f = _lib.FwdArgs()
+    N = n_max + 1
+    f.shape = _lib.make_shape(_lib.DSQG_BF16, 1, H, N, D, offs)
+    st = (ctypes.c_int64 * 4)(N * rs, D, rs, 1)
+    for name in ("q", "k", "v", "out"):
+        setattr(f, name, 0x10000)
+        setattr(f, name + "_stride", st)
+    f.pos_bias = 0x10000
+    assert lib.dsqg_fwd(ctypes.byref(f), None) == _lib.DSQG_EUNSUPPORTED   # refused before a launch

@@ -25,7 +25,7 @@ def test_more_than_one_gpu_is_refused(capsys):
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU exit")
 @pytest.mark.parametrize("argv", [[], ["--decode-sweep"], ["--table-sweep"], ["--profile-kernel", "pool"],
-                                  ["--profile-kernel", "dq", "--profile-se"], ["--probes"]])
+                                  ["--profile-kernel", "dq", "--profile-se"]])
 def test_every_mode_needs_a_gpu(capsys, argv):
     assert _bench().main(argv) == 1
     assert "no ROCm GPU visible" in capsys.readouterr().err

@@ -215,6 +215,25 @@ def test_long_tables_with_scale_embed(gpu_device, offsets, N):
     compare(got, ref, "bf16", case=f"J={len(offsets)} + scale_embed")
 
 
+@pytest.mark.parametrize("offsets", [OFFSETS_J47, OFFSETS_J46])
+def test_n4096_trainer_shape_d32(gpu_device, offsets):
+    """The N=4096 13M trainer's own call at full size: E 256 with H 8 gives HD 32
+    (train/train_4096_13m_condU.py:51-54), batch 8 (:45), the 47-offset table (:89-93; the
+    46-offset table of BASELINE config 3 alongside), dsqg_attention_backend(q, k, v, pos_bias,
+    scale_embed) (:104-105, 157) with the module's IF gain after it.  bf16 B8 H8 N4096 D32
+    selects the <32, true, 14> / <32, true, 13> kernels; scale_embed ~ 0.05 N(0,1),
+    if_gain ~ U(0.8, 1.2)."""
+    J = len(offsets)
+    inp = _rand_inputs(8, 8, 4096, 32, offsets, torch.bfloat16, seed=4096 + J, gains=False)
+    g = torch.Generator().manual_seed(40 + J)
+    inp["scale_embed"] = torch.randn(J, 32, generator=g) * 0.05
+    inp["if_gain"] = torch.rand(8, generator=g) * 0.4 + 0.8
+    _say(f"N=4096 trainer shape B8 H8 N4096 D32 J{J} + scale_embed + IF gain")
+    got = gpu_run(inp, offsets, gpu_device)
+    ref = oracle_chunked(inp, offsets, torch.float32)
+    compare(got, ref, "bf16", case=f"N=4096 trainer B8 H8 N4096 D32 J{J} + scale_embed + if_gain")
+
+
 def test_bf16_table_beyond_the_mfma_kernels_is_rejected(gpu_device):
     """bf16 has one implementation: a table with more than 16 taps beyond the dense window
     (here 47) is refused with DSQG_EUNSUPPORTED before any launch; fp32 still takes it."""

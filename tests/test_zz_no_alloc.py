@@ -77,3 +77,45 @@ def test_noalloc_equals_workspace_backward_twice(gpu_device):
         for name, x, y in zip(("dq", "dk", "dv", "dpos_bias", "dscale_embed", "dscore_gain",
                                "dif_gain"), bl.outputs(), ref):
             assert torch.equal(x, y), f"{name} differs from dsqg_bwd (B{B} H{H} N{N} D{D})"
+
+
+@pytest.mark.gpu
+def test_noalloc_under_graph_capture(gpu_device):
+    """The case the entry point exists for: dsqg_bwd_noalloc recorded into a HIP graph.  One
+    eager call first (the first call on a device takes the scratch address, a query made outside
+    capture), then the call is captured with torch.cuda.graph and replayed three times, with
+    the outputs poisoned and eager work in between; every replay equals dsqg_bwd bit for bit.
+    An eager call leaves the device's free memory and torch's allocation count unchanged."""
+    lib = _lib.load()
+    bl = _case(gpu_device, 2, 12, 2048, 64, True, True, 3)
+    bl.run()
+    torch.cuda.synchronize(gpu_device)
+    ref = [t.clone() for t in bl.outputs()]
+    a = bl.args
+    a.workspace, a.workspace_bytes = None, 0
+    stream = ops._stream(gpu_device)
+    _lib.check(lib.dsqg_bwd_noalloc(ctypes.byref(a), stream), "dsqg_bwd_noalloc (eager)")
+    torch.cuda.synchronize(gpu_device)
+    free0, alloc0 = torch.cuda.mem_get_info(gpu_device)[0], torch.cuda.memory_allocated(gpu_device)
+    _lib.check(lib.dsqg_bwd_noalloc(ctypes.byref(a), stream), "dsqg_bwd_noalloc (eager)")
+    torch.cuda.synchronize(gpu_device)
+    assert torch.cuda.mem_get_info(gpu_device)[0] == free0
+    assert torch.cuda.memory_allocated(gpu_device) == alloc0
+    for x, y in zip(bl.outputs(), ref):
+        assert torch.equal(x, y)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream().cuda_stream
+        _lib.check(lib.dsqg_bwd_noalloc(ctypes.byref(a), ctypes.c_void_p(cap)), "dsqg_bwd_noalloc (capture)")
+    for rep in range(3):
+        for t in bl.outputs():
+            if t.numel():
+                t.fill_(float("nan"))
+        junk = torch.randn(1 << 20, device=gpu_device).sum()  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize(gpu_device)
+        assert torch.isfinite(junk)
+        for name, x, y in zip(("dq", "dk", "dv", "dpos_bias", "dscale_embed", "dscore_gain",
+                               "dif_gain"), bl.outputs(), ref):
+            assert torch.equal(x, y), f"{name} differs from dsqg_bwd on replay {rep}"
