@@ -58,7 +58,7 @@ int hip_status(hipError_t e) { return e == hipSuccess ? DSQG_OK : DSQG_EHIP; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 struct BwdLayout {
-  size_t dpre, part_bias, part_gain, part_if, part_se, se_stage, total;
+  size_t dpre, lrw, part_bias, part_gain, part_if, part_se, se_stage, total;
   int se_slices, se_per;  // two-stage dscale_embed sum: slices of se_per workgroup partials
 };
 
@@ -70,6 +70,10 @@ BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
   BwdLayout L{};
   size_t off = 0;
   L.dpre = off; off = align256(off + sizeof(float) * (size_t)s.B * s.H * s.N);
+  // bf16: the long-range taps' dk/dv weights, a bf16 pair per (b, h, tap, row), from dq to dk/dv.
+  L.lrw = off;
+  if (s.dtype == DSQG_BF16)
+    off = align256(off + sizeof(unsigned) * (size_t)s.B * s.H * s.N * (p.taps.J - p.taps.W - 1));
   L.part_bias = off; off = align256(off + sizeof(float) * nb * s.J);
   L.part_gain = off; if (a.dscore_gain) off = align256(off + sizeof(float) * nb * s.J);
   L.part_if = off; if (a.dif_gain) off = align256(off + sizeof(float) * nb);
@@ -217,6 +221,7 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream, boo
   p.dk = a->dk; p.dks = to_strides(a->dk_stride);
   p.dv = a->dv; p.dvs = to_strides(a->dv_stride);
   p.dpre = reinterpret_cast<float*>(ws + L.dpre);
+  p.lrw = reinterpret_cast<float*>(ws + L.lrw);
   p.part_bias = reinterpret_cast<float*>(ws + L.part_bias);
   p.part_gain = a->dscore_gain ? reinterpret_cast<float*>(ws + L.part_gain) : nullptr;
   p.part_if = a->dif_gain ? reinterpret_cast<float*>(ws + L.part_if) : nullptr;

@@ -11,18 +11,21 @@
 //    B operand of dK^T = Q^T (c g dS) and dV^T = dOut^T (a alpha); Q^T and dOut^T come from the
 //    query window [m0, m0+96) in LDS through ds_read_tr16_b64.
 //  * Long-range taps: query rows m0w + delta + 0..15, loaded whole-row (D/8 lanes per row: the
-//    vector L1 serves that at close to four times the rate of the MFMA operand order); q.k,
-//    dOut.v and q.se_j are VALU dot products (v_dot2_f32_bf16, DPP sums over the row's lanes)
-//    handed to the lanes of key column i through LDS.  The query / dOut rows are staged in the
-//    wave's rows of the (by then free) window tiles; each tap's diagonal update is one
-//    v_mfma_f32_16x16x32_bf16 per 16 head dims whose k runs over the 16 staged rows twice, against
-//    a one-hot operand holding the weight as bf16 hi (k = i) and lo (k = 16 + i), so the weight
-//    keeps its fp32 precision.  The LDS fits four workgroups per CU (three with scale_embed).
+//    vector L1 serves that at close to four times the rate of the MFMA operand order).  Their
+//    weights come from launch 1, which has every long-range pair's alpha, u and D' in hand
+//    anyway: per (query, tap) the pair (c g_j dS_j, a alpha_j) as two bf16 in one dword, read
+//    by the lane on key i's diagonal, so this launch computes no long-range score and reads no
+//    long-range lse or D'.  The query / dOut rows are staged in the wave's rows of the (by then
+//    free) window tiles; each tap's diagonal update is one v_mfma_f32_16x16x16_bf16 per 16 head
+//    dims and matrix: a transposed read of the staged rows against a one-hot operand holding the
+//    weight.  (Each of these 11 of the 44 terms of dk and dv carries the 2^-9 relative rounding
+//    of one bf16 weight; the band's 33 keep fp32 weights as hi + lo pairs.)  The LDS fits four
+//    workgroups per CU (three with scale_embed).
 //  * The dense band's weights enter their MFMAs as bf16 hi + lo pairs (two products each).
-//  * The q.se_j term of the score (scale_embed) is a [query][tap] table per wave computed on the
-//    MFMA (Q SE^T) for the band, and a short dot product for the long-range taps, both with se
-//    rounded to bf16 (an error of about 2^-9 |c q.se| in the score, 1e-4 at the reference's
-//    se ~ 0.05; the parameter gradients come from launch 1, which keeps se at fp32 precision).
+//  * The q.se_j term of the band's scores (scale_embed) is a [query][tap] table per wave computed
+//    on the MFMA (Q SE^T) with se rounded to bf16 (an error of about 2^-9 |c q.se| in the score,
+//    1e-4 at the reference's se ~ 0.05; the parameter gradients come from launch 1, which keeps
+//    se at fp32 precision).
 // With p.red_blocks > 0 the launch carries that many extra workgroups at the end of the grid,
 // which sum the parameter-gradient partials (dsqg_reduce.hpp) while the dk/dv tiles run.
 // Follows _bwd_dkdv_v3 (kernels/dsqg_attention_v3.py:282-352).
@@ -61,7 +64,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain2[kMaxTaps];                 // gain * c * log2e
   __shared__ float sGainC[kMaxTaps];                 // gain * c
-  __shared__ float2 sPair[4][16];                    // per wave: long-range (score, dOut.v) of one tap
 
   const int tid = threadIdx.x;
   // Workgroups past the dk/dv tiles run the parameter reduction (partials from launch 1).
@@ -105,14 +107,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
   int dl_s[NSM];
   load_sparse_deltas(p.taps, dl_s);
   const int klane = opaque(i * ksn + 8 * g), vlane = opaque(i * vsn + 8 * g);
-  // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
-  int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
+  // Row-chunk layout (whole rows per D/8 lanes) for the long-range query / dOut rows.
+  int qlaneR[CHW], olaneR[CHW];
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
     qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
     olaneR[u] = opaque(rc_lane<D>(l, u, dosn));
-    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
-    vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
   }
 
   // ---- Loads (scale_embed first: the T table waits for it alone). ----
@@ -139,12 +139,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     kB[s] = as_bf16x8(bload16(rK, m0w * ksn + (sv ? klane + 32 * s : kNoElem)));
     vB[s] = as_bf16x8(bload16(rV, m0w * vsn + (sv ? vlane + 32 * s : kNoElem)));
   }
-  uint4 kR[CHW], vR[CHW];
-#pragma unroll
-  for (int u = 0; u < CHW; ++u) {
-    kR[u] = bload16(rK, m0w * ksn + klaneR[u]);
-    vR[u] = bload16(rV, m0w * vsn + vlaneR[u]);
-  }
   // lse (log2 units) and D' of the band's queries m0w + 16qb + 4g + r.
   float lq[12], dq_[12];
 #pragma unroll
@@ -155,14 +149,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
       lq[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
       dq_[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
     }
-  // lse and D' of the query on this lane's diagonal for the long-range taps (query m + delta;
-  // lanes off the diagonal fetch a harmless value), in a ring PF taps ahead like the query rows.
-  constexpr int LPF = PF;
-  float lseS[LPF], dpS[LPF];
-  auto load_lse = [&](int t) {
-    const int nq = m + dl_s[t];
-    lseS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
-    dpS[t % LPF] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
+  // Weights of the long-range taps from launch 1, for the query on this lane's diagonal (query
+  // m + delta; lanes off the diagonal read past the buffer and get zeros), PF taps ahead like the
+  // query rows.  One buffer resource per tap: the [N] dwords of the (b,h) and tap, so a query at
+  // or past N reads as a zero weight.
+  const bool diag = g == (i >> 2);
+  const unsigned* const lwb = reinterpret_cast<const unsigned*>(p.lrw) + (long long)bh * NS * N;
+  unsigned wS[PF];
+  auto load_w = [&](int t) {
+    const __amdgpu_buffer_rsrc_t rW =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(lwb + (long long)t * N), (short)0, N * 4, 0x00020000);
+    const unsigned off = diag ? (unsigned)(m + dl_s[t]) * 4u : 0x80000000u;
+    wS[t % PF] = __builtin_amdgcn_raw_buffer_load_b32(rW, off, 0, 0);
   };
 
   if (tid < J) {
@@ -257,8 +255,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
   // Their first loads are issued only now: during the band the registers hold the band's
   // operands, and four workgroups per CU cover the wait.
 #pragma unroll
-  for (int t = 0; t < LPF; ++t)
-    if (NSC > 0 ? t < NSC : t < NS) load_lse(t);
+  for (int t = 0; t < PF; ++t)
+    if (NSC > 0 ? t < NSC : t < NS) load_w(t);
   // Long-range query / dOut rows m0w + delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
   uint4 qS[PF][CHW], oS[PF][CHW];
 #pragma unroll
@@ -272,9 +270,6 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
       }
     }
   }
-  // One-hot weights of the long-range taps: key i's weight in the diagonal lane (i, i / 4),
-  // element i % 4 (the B operand of the 16x16x16 products below); other lanes contribute zeros.
-  const bool diag = g == (i >> 2);
   // The wave's long-range query / dOut rows are staged in the window tiles (rows 16w..16w+15),
   // free once every wave's band is done.
   bf16_t* qsw = sQ + w * 16 * RV;
@@ -285,33 +280,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
-      const int j = W + 1 + t;
-      const int dl = dl_s[t];
-      // This tap's lse / D' (taken before the ring slot is refilled for tap t + PF).
-      const float lseq = lseS[t % LPF], dpq = dpS[t % LPF];
-      // The score's dot products (gain c log2e q.k + c log2e q.se_j) and dOut.v on the VALU:
-      // each lane dots its 16-byte chunk, the row's lanes sum (DPP), and one lane per row hands
-      // the pair to the diagonal lane through LDS.  The query / dOut rows are staged (natural
-      // row order) for the transposing reads.
+      // This tap's weights (taken before the ring slot is refilled for tap t + PF).
+      const unsigned wt = wS[t % PF];
 #pragma unroll
       for (int u = 0; u < CHW; ++u) {
-        float sk = sGain2[j] * dot8_bf16(qS[t % PF][u], kR[u], 0.f);
-        if constexpr (HAS_SE) {
-          // Lanes past the row read chunk 0 (finite) against their zero query chunk.
-          const int sc8 = rc_valid<D>(l, u) ? rc_chunk<D>(l, u) * 8 : 0;
-          const uint4 se = *reinterpret_cast<const uint4*>(sSE + j * RV + sc8);
-          sk = fmaf(c2, dot8_bf16(qS[t % PF][u], se, 0.f), sk);
-        }
-        const float dk = group_sum<CPRP>(sk);
-        const float dv = group_sum<CPRP>(dot8_bf16(oS[t % PF][u], vR[u], 0.f));
         if (rc_valid<D>(l, u)) {
           st16(qsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qS[t % PF][u]);
           st16(osw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, oS[t % PF][u]);
         }
-        if (rc_chunk<D>(l, u) == 0) sPair[w][rc_row<D>(l, u)] = float2{dk, dv};
       }
       if (t + PF < NS) {
-        load_lse(t + PF);
+        load_w(t + PF);
         const int n0 = m0w + dl_s[t + PF];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) {
@@ -319,26 +298,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
           oS[t % PF][u] = bload16(rO, n0 * dosn + olaneR[u]);
         }
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and results are written
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged rows are written
       __builtin_amdgcn_wave_barrier();
-      const float2 pr = sPair[w][i];
-      const int nq = m + dl;  // the query on this lane's diagonal (lanes off the diagonal: unused)
-      const bool ok = key_ok && nq < N;
-      const float uval = pr.y;
-      const float alpha = ok ? __builtin_amdgcn_exp2f(pr.x + sBias2[j] - lseq) : 0.f;
-      const float dS = a * alpha * (uval - dpq);
-      // The weights as bf16 hi + lo pairs (fp32 precision of the products); each transposed
-      // read of the staged rows feeds two 16x16x16 products, hi and lo.
-      s16x4_t bk, bkl, bv, bvl;
-      split_onehot_bf16x4(diag ? sGainC[j] * dS : 0.f, i & 3, bk, bkl);
-      split_onehot_bf16x4(diag ? a * alpha : 0.f, i & 3, bv, bvl);
+      // One-hot weights: key i's in the diagonal lane (i, i / 4), element i % 4 (the other
+      // lanes hold zeros), the dk weight from the low half of the dword, the dv weight from the
+      // high half.
+      const s16x4_t bk = onehot_bf16_bits(wt & 0xffffu, i & 3);
+      const s16x4_t bv = onehot_bf16_bits(wt >> 16, i & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
         const s16x4_t qt = lds_read_tr16(qtr + 16 * db), ot = lds_read_tr16(otr + 16 * db);
         dK[db] = mfma_16x16x16(qt, bk, dK[db]);
-        dK[db] = mfma_16x16x16(qt, bkl, dK[db]);
         dV[db] = mfma_16x16x16(ot, bv, dV[db]);
-        dV[db] = mfma_16x16x16(ot, bvl, dV[db]);
       }
     }
   }

@@ -24,6 +24,10 @@
 // so these products keep fp32 precision as in the reference (kernels/dsqg_attention_v3.py:
 // 257-271 sums dq and dse in fp32).
 //
+// Every long-range pair's dk/dv weights, bf16(c g_j dS_j) and bf16(a alpha_j), also go to the
+// workspace ([b,h][tap][query] dwords) for launch 2, so that the key-centric pass needs no
+// long-range score, lse or D' of its own.
+//
 // Follows _compute_D_v3 + _bwd_dq_v3 (kernels/dsqg_attention_v3.py:170-275), except that D' is
 // computed from the fp32 weights and the parameter gradients avoid atomics.
 #include "dsqg_common.hpp"
@@ -439,10 +443,16 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
         }
       }
     if (diag) {
+      // The long-range taps' dk/dv weights go to the workspace for launch 2, which then needs
+      // neither the taps' dot products nor their queries' lse and D': [b,h][tap][query] dwords
+      // holding bf16(c g_j dS_j) (low half) and bf16(a alpha_j) (high half), zero for a masked tap.
+      unsigned* const lw = reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N + n;
 #pragma unroll
       for (int t = 0; t < NSM; ++t)
         if (NSC > 0 || t < NS) {
-          sDSw[i * TS + W + 1 + t] = a * als[t] * (uus[t] - Dp);
+          const float ds = a * als[t] * (uus[t] - Dp);
+          sDSw[i * TS + W + 1 + t] = ds;
+          if (row_ok) lw[(long long)t * N] = cvt_pk_bf16(c * sGain[W + 1 + t] * ds, a * als[t]);
         }
     }
     if (g == 0) sDpw[i] = row_ok ? Dp : 0.f;

@@ -172,6 +172,11 @@ struct BwdParams {
   float* part_se;     // workspace [B*H*n_chunks][J][D] or null
   float* part_gain;   // workspace [B*H*n_chunks][J] or null
   float* part_if;     // workspace [B*H*n_chunks] or null
+  // bf16 MFMA path: the long-range taps' weights, written by dq and read by dk/dv, workspace
+  // [B*H][NS][N] dwords (NS = taps beyond the dense window), for query n and tap W + 1 + t:
+  // low half bf16(c g_j dS_j) (the weight of q_n in dk), high half bf16(a alpha_j) (the weight
+  // of dOut_n in dv).
+  float* lrw;
   // Parameter reduction run by red_blocks extra workgroups of the bf16 dk/dv launch (0: none).
   ReduceParams red;
   int red_blocks;

@@ -173,6 +173,11 @@ __device__ __forceinline__ void split_bf16x4(float a, float b, float c, float d,
   lo = __builtin_bit_cast(s16x4_t, make_uint2(cvt_pk_bf16(a - ha, b - hb), cvt_pk_bf16(c - hc, d - hd)));
 }
 
+// A bf16 bit pattern (low 16 bits of bits) placed as a one-hot operand at element e.
+__device__ __forceinline__ s16x4_t onehot_bf16_bits(unsigned bits, int e) {
+  return __builtin_bit_cast(s16x4_t, (unsigned long long)bits << (16 * e));
+}
+
 // The split of x placed as a one-hot operand pair at element e (shifts of 16 e bits).
 __device__ __forceinline__ void split_onehot_bf16x4(float x, int e, s16x4_t& hi, s16x4_t& lo) {
   const __bf16 hb = (__bf16)x;

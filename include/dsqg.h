@@ -167,9 +167,11 @@ int dsqg_bwd(const dsqg_bwd_args* args, dsqg_stream_t stream);
 
 /* The three phases dsqg_bwd runs, for callers that launch them separately (the reference's
  * backward is likewise three launches: kernels/dsqg_attention_v3.py:397-441).  Call them in
- * this order on one stream with the same args and workspace: the workspace carries D' and the
- * parameter-gradient partials from phase 1 to phases 2 and 3.
- *  - dsqg_bwd_dq     <- _compute_D_v3 + _bwd_dq_v3 (:397-424): dq, D', partials
+ * this order on one stream with the same args and workspace: the workspace carries D', (bf16)
+ * the long-range taps' dk/dv weights and the parameter-gradient partials from phase 1 to
+ * phases 2 and 3.
+ *  - dsqg_bwd_dq     <- _compute_D_v3 + _bwd_dq_v3 (:397-424): dq, D', partials, and for bf16
+ *                       the weights (c g dS, a alpha) of every query's long-range taps
  *  - dsqg_bwd_dkdv   <- _bwd_dkdv_v3 (:426-441): dk, dv
  *  - dsqg_bwd_params <- the tl.atomic_add accumulation of dpb/dse in _bwd_dq_v3 (:265-271),
  *                       here a deterministic reduction of the partials */
