@@ -280,7 +280,8 @@ def table_sweep(dev, reps=50):
             pb = torch.randn((J, H), generator=gen, device=dev) * 0.5
             fl = ops.FwdLaunch(q, k, v, pb, None, None, None, list(offs))
             fl.run()
-            bl = ops.BwdLaunch(q, k, v, do, fl.lse, pb, None, None, None, list(offs), False, False, False)
+            bl = ops.BwdLaunch(q, k, v, do, fl.lse, pb, None, None, None, list(offs), False, False, False,
+                               alpha_lr=fl.alpha_lr)
             sets.append((fl, bl))
         for i in range(10):
             sets[i % 2][0].run()
@@ -506,7 +507,7 @@ def profile_mode(args, w, dev):
         bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
                            d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
                            d["scale_embed"] is not None, d["score_gain"] is not None,
-                           d["if_gain"] is not None)
+                           d["if_gain"] is not None, alpha_lr=fl.alpha_lr)
     fl.run()
     bl.run()
     torch.cuda.synchronize()
@@ -569,7 +570,7 @@ def make_sets(w, dev, n, scale_embed=False, if_gain=False):
         bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
                            d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
                            d["scale_embed"] is not None, d["score_gain"] is not None,
-                           d["if_gain"] is not None)
+                           d["if_gain"] is not None, alpha_lr=fl.alpha_lr)
         sets.append((inp if i == 0 else None, d, fl, bl))
     return sets
 

@@ -16,7 +16,7 @@ PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("DSQG_HIP_LIB", PKG_DIR / "libdsqg_hip.so"))
 
 MAX_OFFSETS = 64
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DSQG_OK, DSQG_EINVAL, DSQG_EUNSUPPORTED, DSQG_EHIP, DSQG_EWORKSPACE = 0, 1, 2, 3, 4
 DSQG_ETOOLARGE = 5
@@ -40,7 +40,7 @@ class FwdArgs(ctypes.Structure):
                 ("v", _vp), ("v_stride", _i64x4),
                 ("pos_bias", _vp), ("scale_embed", _vp), ("score_gain", _vp), ("if_gain", _vp),
                 ("out", _vp), ("out_stride", _i64x4),
-                ("lse", _vp)]
+                ("lse", _vp), ("alpha_lr", _vp)]
 
 
 class BwdArgs(ctypes.Structure):
@@ -56,7 +56,8 @@ class BwdArgs(ctypes.Structure):
                 ("dv", _vp), ("dv_stride", _i64x4),
                 ("dpos_bias", _vp), ("dscale_embed", _vp), ("dscore_gain", _vp),
                 ("dif_gain", _vp),
-                ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t)]
+                ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+                ("alpha_lr", _vp)]
 
 
 class DecodeArgs(ctypes.Structure):
@@ -98,6 +99,8 @@ SIGNATURES = {
     "dsqg_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "dsqg_supported_head_dims": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int32), ctypes.c_int]),
     "dsqg_fwd": (ctypes.c_int, [ctypes.POINTER(FwdArgs), _vp]),
+    "dsqg_long_range_taps": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int32), ctypes.c_int]),
+    "dsqg_alpha_lr_elems": (ctypes.c_int, [ctypes.POINTER(Shape), ctypes.POINTER(ctypes.c_size_t)]),
     "dsqg_bwd_workspace_size": (ctypes.c_int, [ctypes.POINTER(BwdArgs),
                                                ctypes.POINTER(ctypes.c_size_t)]),
     "dsqg_bwd": (ctypes.c_int, [ctypes.POINTER(BwdArgs), _vp]),
@@ -172,3 +175,12 @@ def _shape_cached(dtype_code: int, B: int, H: int, N: int, D: int, offsets: tupl
     for i, o in enumerate(offs):
         s.offsets[i] = int(o)
     return s
+
+
+def long_range_taps(offsets) -> int:
+    """Taps beyond the dense window of an offset table (the NS of the forward's alpha_lr)."""
+    arr = (ctypes.c_int32 * len(offsets))(*offsets)
+    ns = load().dsqg_long_range_taps(arr, len(offsets))
+    if ns < 0:
+        raise DSQGLibraryError(f"dsqg_long_range_taps: {status_string(-ns)}")
+    return ns

@@ -77,7 +77,7 @@ def dsqg_attention(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
     q, k, v = _compute_dtype(q, k, v)
     args = (q, k, v, pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain),
             list(offs))
-    out, _ = ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args)
+    out = (ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args))[0]
     return out if out.dtype == orig else out.to(orig)
 
 
@@ -104,7 +104,7 @@ def dsqg_attention_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor,
     params = (pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain), list(offs))
     if kv_inject is None:
         args = (qkv, num_heads, *params)
-        out, _ = ops.dsqg_fwd_qkv(*args) if ops.traced(qkv) else ops.AttentionQkvFn.apply(*args)
+        out = (ops.dsqg_fwd_qkv(*args) if ops.traced(qkv) else ops.AttentionQkvFn.apply(*args))[0]
     else:
         k_delta, v_delta = kv_inject
         assert k_delta.shape == k.shape and v_delta.shape == v.shape, \
@@ -141,7 +141,7 @@ def dsqg_attention_with_lse(q, k, v, pos_bias, scale_embed=None, *, offsets=None
     q, k, v = _compute_dtype(q, k, v)
     args = (q, k, v, pos_bias.float(), _f32(scale_embed), _f32(score_gain), _f32(if_gain),
             list(offs))
-    out, lse = ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args)
+    out, lse = (ops.dsqg_fwd(*args) if ops.traced(q, k, v) else ops.AttentionFn.apply(*args))[:2]
     return (out if out.dtype == orig else out.to(orig)), lse
 
 

@@ -103,6 +103,10 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   if ((st = check_tensor(a->dk, a->dk_stride, s.dtype, ne))) return st;
   if ((st = check_tensor(a->dv, a->dv_stride, s.dtype, ne))) return st;
   if (ne > 0 && !a->lse) return DSQG_EINVAL;
+  // bf16: the forward's long-range weights (4-byte aligned fp32) whenever there are such taps.
+  if (s.dtype == DSQG_BF16 && ne > 0 && p->taps.J - p->taps.W - 1 > 0 &&
+      (!a->alpha_lr || (reinterpret_cast<uintptr_t>(a->alpha_lr) & 3u) != 0))
+    return DSQG_EINVAL;
   if ((long long)s.J * s.H > 0 && (!a->pos_bias || !a->dpos_bias)) return DSQG_EINVAL;
   if (!aligned16(a->scale_embed)) return DSQG_EINVAL;  // read as 16-byte pieces
   p->B = s.B; p->H = s.H; p->N = s.N;
@@ -169,10 +173,36 @@ int dsqg_fwd(const dsqg_fwd_args* a, dsqg_stream_t stream) {
   p.score_gain = a->score_gain; p.if_gain = a->if_gain;
   p.out = a->out; p.os = to_strides(a->out_stride);
   p.lse = a->lse;
+  p.alpha_lr = s.dtype == DSQG_BF16 ? a->alpha_lr : nullptr;
   // bf16 has one implementation, the MFMA kernel: tables with more long-range taps than it
   // holds, or slices beyond its 32-bit offsets, are not taken.
   if (s.dtype == DSQG_BF16 && !fwd_mfma_supported(p, s.D)) return DSQG_EUNSUPPORTED;
   return hip_status(launch_fwd(p, s.dtype, s.D, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int dsqg_long_range_taps(const int32_t* offsets, int J) {
+  if (!offsets) return -DSQG_EINVAL;
+  dsqg_shape s;
+  memset(&s, 0, sizeof(s));
+  s.dtype = DSQG_BF16; s.D = 64; s.J = J;
+  if (J < 1 || J > DSQG_MAX_OFFSETS) return -DSQG_EINVAL;
+  for (int j = 0; j < J; ++j) s.offsets[j] = offsets[j];
+  TapTable taps;
+  const int st = check_shape(s, true, &taps);
+  if (st == DSQG_EINVAL) return -DSQG_EINVAL;
+  int W = 0;
+  while (W + 1 < J && W + 1 <= kMaxWindow && offsets[W + 1] == W + 1) ++W;
+  return J - W - 1;
+}
+
+int dsqg_alpha_lr_elems(const dsqg_shape* shape, size_t* elems) {
+  if (!shape || !elems) return DSQG_EINVAL;
+  TapTable taps;
+  const int st = check_shape(*shape, true, &taps);
+  if (st) return st;
+  *elems = shape->dtype == DSQG_BF16
+               ? (size_t)shape->B * shape->H * shape->N * (size_t)(taps.J - taps.W - 1) : 0;
+  return DSQG_OK;
 }
 
 int dsqg_bwd_workspace_size(const dsqg_bwd_args* a, size_t* bytes) {
@@ -215,6 +245,7 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream, boo
   p.v = a->v; p.vs = to_strides(a->v_stride);
   p.dout = a->dout; p.dos = to_strides(a->dout_stride);
   p.lse = a->lse;
+  p.alpha_lr = a->alpha_lr;
   p.pos_bias = a->pos_bias; p.scale_embed = a->scale_embed;
   p.score_gain = a->score_gain; p.if_gain = a->if_gain;
   p.dq = a->dq; p.dqs = to_strides(a->dq_stride);

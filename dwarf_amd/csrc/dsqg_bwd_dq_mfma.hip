@@ -1,32 +1,33 @@
-// DSQG backward, launch 1, bf16 MFMA path (gfx950): query-centric dq, D' and the per-workgroup
-// parameter-gradient partials.
+// DSQG backward, launch 1, bf16 MFMA path (gfx950): query-centric dq, D', the long-range taps'
+// dk/dv weights and the per-workgroup parameter-gradient partials.
 //
-// A workgroup owns one (b,h) and a run of 64-row query tiles; wave w owns rows n0+16w .. +15 of
-// the tile.  With lse from the forward, every weight alpha_j = exp(s_j - lse) is known as soon
-// as its score is, so the taps stream through once:
-//   u_j   = dOut . v_j                      (U^T = V dOut^T on the MFMA, like S^T = K Q^T)
-//   D'   += alpha_j u_j
-//   X    += g_j alpha_j (u_j - D0) k_j,   Y += g_j alpha_j k_j   (K^T from LDS, ds_read_tr16_b64)
-// and at the end dq = c (a (X - (D' - D0) Y) + sum_j dS_j se_j) with dS_j = a alpha_j (u_j - D').
-// This is sum_j dS_j (c g_j k_j + c se_j), the gradient of s_j = c g_j q.k_j + b_j + c q.se_j.
-// D0, the dense band's alpha-weighted mean of u, is known before the first product; taking it
-// out of u before the bf16 rounding of the operands keeps their error proportional to u - D'.
-// The dense band and the long-range taps are laid out as in the forward (dsqg_fwd_mfma.hip):
-// band keys [n0w-32, n0w+16) as three 16x16 tiles, long-range taps as the diagonal of one tile.
-// dS is then written to a per-wave [query][tap] table in LDS, from which the workgroup sums
-// dbias (and dg, da) in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS over
-// the tile's 64 queries, its [D x J] output tiles split over the four waves).
-// With scale_embed the q.se_j term is an MFMA (SE Q^T): for the dense taps filed in a per-wave
-// [query][tap] table that shares the wave's staging block, for the long-range taps in their dS
-// table slots until the diagonal lane reads them.  scale_embed is staged as two bf16 planes
-// (hi = bf16(se), lo = bf16(se - hi)), and every weight that enters an MFMA (the dense band's
-// and the one-hot long-range X / Y weights, dS in dse and in SE^T dS^T) is split the same way,
-// so these products keep fp32 precision as in the reference (kernels/dsqg_attention_v3.py:
-// 257-271 sums dq and dse in fp32).
-//
-// Every long-range pair's dk/dv weights, bf16(c g_j dS_j) and bf16(a alpha_j), also go to the
-// workspace ([b,h][tap][query] dwords) for launch 2, so that the key-centric pass needs no
-// long-range score, lse or D' of its own.
+// A workgroup owns one (b,h) and 64 query rows [n0, n0+64); wave w owns rows n0w = n0+16w .. +15.
+// With lse from the forward, every weight alpha_j = exp(s_j - lse) is known as soon as its
+// score is, and the forward also stored the long-range taps' weights (alpha_lr), so:
+//  1. Dense band (delta = 0..W): keys [n0w-32, n0w+16) as three 16x16 tiles, S^T = K Q^T and
+//     U^T = V dOut^T on the MFMA (v_mfma_f32_16x16x32_bf16), alpha_j from S and lse, u_j = U.
+//  2. Long-range pass 1, V rows only: u_j = dOut . v_j for tap j's 16 value rows n0w - delta + 0..15,
+//     gathered whole-row (D/8 lanes per row) and dotted on the VALU (v_dot2_f32_bf16, DPP sums
+//     over the row's lanes); each row's u goes to the wave's [query][tap] table in LDS without a
+//     wait per tap.  Then D' = sum_j alpha_j u_j (= dOut . o, pre-gain o) is exact (fp32 weights).
+//  3. With D' known, dS_j = a alpha_j (u_j - D') and dq = c sum_j dS_j (g_j k_j + se_j):
+//     the band's part as MFMAs K^T (c g dS)^T with K^T from LDS (ds_read_tr16_b64), then
+//     long-range pass 2, K rows only: each tap's 16 key rows (gathered whole-row) are staged in
+//     the wave's LDS block and read back transposed against a one-hot operand held by the
+//     query's diagonal lane.  Every weight enters its MFMA as a bf16 hi + lo pair, so the
+//     products keep fp32 weights, as the reference's fp32 sums do (kernels/dsqg_attention_v3.py:
+//     257-271).
+//  4. dS fills the per-wave [query][tap] table, from which the workgroup sums dbias (and dg, da)
+//     in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS over the tile's 64 queries,
+//     its [D x J] output tiles split over the four waves).  Every long-range pair's dk/dv weights,
+//     bf16(c g_j dS_j) and bf16(a alpha_j), go to the workspace ([b,h][tap][query] dwords) for
+//     launch 2, so the key-centric pass needs no long-range score, lse or D' of its own.
+// With scale_embed the band's q.se_j term is an MFMA (SE Q^T) filed in a per-wave [query][tap]
+// table; se is staged as two bf16 planes (hi = bf16(se), lo = bf16(se - hi)) and dS in SE^T dS^T
+// and in dse is split the same way, so these products carry se and dS at fp32 precision.
+// The long-range taps' scores are not recomputed: their alpha comes from the forward.  With the
+// score gain's gradient requested, c q.k of every pair is also needed: the band's from S, the
+// long-range taps' from a dot product with the staged key rows in pass 2.
 //
 // Follows _compute_D_v3 + _bwd_dq_v3 (kernels/dsqg_attention_v3.py:170-275), except that D' is
 // computed from the fp32 weights and the parameter gradients avoid atomics.
@@ -45,7 +46,8 @@ constexpr int kDqTableStride = 52;
 // DG: the score gain's gradient is requested (its c q.k table in dynamic LDS and the extra row
 // sums are compiled in only then).
 template <int D, bool HAS_SE, int NSC, bool DG>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC != 11) ? 2 : 3)) void bwd_dq_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC != 11) ? 2 : (HAS_SE || DG ? 3 : 4)))
+void bwd_dq_mfma_kernel(BwdParams p) {
   using G_ = Geo<D>;
   constexpr int QT = 64;
   constexpr int KS = G_::KS;
@@ -58,13 +60,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
   constexpr int CPRP = G_::CPRP;          // lanes per row in the row-chunk layout
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
-  constexpr int PF = 2;                   // long-range K/V operands loaded ahead of use
+  constexpr int PF = 2;                   // long-range row blocks loaded ahead of use
   constexpr int TS = kDqTableStride;
   constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
   constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
   constexpr int SEJ = 48;                 // scale_embed rows staged (J <= 48)
   constexpr int NTSE = 3 * DB;            // 16x16 tiles of dse^T [D x 48]
   constexpr int TPW = (NTSE + 3) / 4;     // ... per wave
+  constexpr bool QROWS = HAS_SE || DG;    // the query rows are needed whole-row (dse, long-range q.k)
   constexpr float kLog2e = 1.4426950408889634f;
 
   __shared__ __align__(16) bf16_t sK[WIN * RV];        // dense-window K rows
@@ -77,18 +80,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   // SE^T dS then carry se to about 2^-17 relative, as the fp32 se of the reference.
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
   __shared__ __align__(16) bf16_t sSElo[HAS_SE ? SEJ * RV : 8];
-  // dS[query][tap] per wave; with scale_embed it lives in the V window once the band is done
-  // (D >= 64), which leaves room for three workgroups per CU.
-  constexpr bool TBL_IN_V = HAS_SE && WIN * RV * 2 >= 4 * 16 * TS * 4;
+  // [query][tap] per wave: u of the long-range taps (pass 1), then dS.  It lives in the V window
+  // once the band is done (D >= 64), which keeps the workgroup's LDS small enough for four
+  // workgroups per CU (three with scale_embed).
+  constexpr bool TBL_IN_V = WIN * RV * 2 >= 4 * 16 * TS * 4;
   __shared__ __align__(16) float sDSst[TBL_IN_V ? 4 : 4 * 16 * TS];
   // c q.k per (query, tap), for dg only: dynamic LDS, present when score_gain's gradient is
-  // requested (without it the workgroup fits three per CU).
+  // requested.
   extern __shared__ __align__(16) float sDyn[];
   float* const sRAW = sDyn;
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain[kMaxTaps];
-  // Per wave, one long-range tap's row results (q.k, dOut.v).
-  __shared__ __align__(16) float sPair[4][16][2];
+  __shared__ float sDp[4][16];            // per wave: D' of its rows (the da sum)
 
   const int tid = threadIdx.x;
   // The kernel arguments of the prologue in one round trip: sizes and input strides pass through
@@ -100,9 +103,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   asm volatile("" : "+s"(nblk), "+s"(p.H), "+s"(p.N), "+s"(p.n_chunks), "+s"(p.taps.J), "+s"(p.taps.W),
                "+s"(p.qs.b), "+s"(p.qs.h), "+s"(p.qs.n), "+s"(p.ks.b), "+s"(p.ks.h), "+s"(p.ks.n),
                "+s"(p.vs.b), "+s"(p.vs.h), "+s"(p.vs.n), "+s"(p.dos.b), "+s"(p.dos.h), "+s"(p.dos.n)
-               : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.dout), "s"(p.lse), "s"(p.pos_bias), "s"(p.if_gain));
+               : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.dout), "s"(p.lse), "s"(p.pos_bias), "s"(p.if_gain),
+                 "s"(p.alpha_lr));
   const int lb = xcd_logical_block(blockIdx.x, nblk);
-  const int bh = lb / p.n_chunks, chunk = lb - bh * p.n_chunks;
+  const int bh = lb / p.n_chunks, tile = lb - bh * p.n_chunks;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;
   const int NS = NSC > 0 ? NSC : J - W - 1;
@@ -120,6 +124,13 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
   const long long rowbase = ((long long)b * p.H + h) * N;
 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 15, g = l >> 4;
+  const int n0 = tile * QT;
+  const int n0w = n0 + 16 * w;
+  const int n = n0w + i;  // query row of this lane's MFMA column
+  const bool row_ok = n < N;
+  // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the
+  // one-hot operand of the long-range dq products must sit there.
+  const bool diag = g == (i >> 2);
   const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
   // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
   int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
@@ -130,6 +141,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
     klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
     vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
   }
+  int dl_s[NSM];
+  load_sparse_deltas(p.taps, dl_s);
 
   // Per-tap bias and gain (J <= kMaxTaps < kBlock: one per thread).  With scale_embed they are
   // staged here, with the scale_embed rows, all requested before the one wait: held in registers
@@ -153,412 +166,356 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 || (HAS_SE && NSC !=
 
   float* const sDS = TBL_IN_V ? reinterpret_cast<float*>(sV) : sDSst;
   // Table columns J..47 are read as zeros (whole 4-wide groups feed the MFMA operands); a table
-  // in the V window gets them after the band.
-  // Thread t clears row t % 64 from column J + t / 64 on, every fourth column.
+  // in the V window gets them after the band.  Thread t clears row t % 64 from column J + t / 64
+  // on, every fourth column.
   for (int j = J + (tid >> 6); j < 48; j += kBlock / 64) {
     if (!TBL_IN_V) sDS[(tid & 63) * TS + j] = 0.f;
     if (g_grad) sRAW[(tid & 63) * TS + j] = 0.f;
   }
+  float* sDSw = sDS + w * 16 * TS;
+  float* sRAWw = sRAW + w * 16 * TS;  // dereferenced only when g_grad
+  bf16_t* sKsw = sKs[w];
+  float* sTw = reinterpret_cast<float*>(sKsw);
 
+  // ---- Loads (zero outside [0, N)). ----
+  // Dense window K and V rows [n0-32, n0+64), staged once per workgroup in LDS.
+  uint4 wk[CWIN], wv[CWIN];
+#pragma unroll
+  for (int u = 0; u < CWIN; ++u) {
+    const int ci = tid + u * kBlock;
+    const bool cv = ci % CPS < CPR;
+    wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
+    wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
+  }
+  if constexpr (!HAS_SE) {
+    bias_ld = p.pos_bias[jc * p.H + h];
+    gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
+  }
+  bf16x8_t qB[KS], oB[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const bool sv = 8 * g + 32 * s < D;  // the zero columns of D = 80's last K-step
+    qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (sv ? qlane + 32 * s : kNoElem)));
+    oB[s] = as_bf16x8(bload16(rO, n0w * dosn + (sv ? olane + 32 * s : kNoElem)));
+  }
+  uint4 oR[CHW];
+  [[maybe_unused]] uint4 qR[QROWS ? CHW : 1];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    oR[u] = bload16(rO, n0w * dosn + olaneR[u]);
+    if constexpr (QROWS) qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
+  }
+  // Unconditional (a row past N reads row N - 1 and is masked below): a load under the row
+  // test was waited for inside the branch, before the long-range loads could be issued.
+  const float lse_ld = p.lse[rowbase + (row_ok ? n : N - 1)];
+  // The forward's long-range weights of this lane's query ([b,h][tap][query] fp32), on the
+  // diagonal lane (the others read past the buffer and get zeros); one buffer resource per tap
+  // over its [N] row weights, so a row past N reads as zero too.
+  float als[NSM];
+  {
+    const float* const alb = p.alpha_lr + (long long)bh * NS * N;
+    const unsigned off = diag ? (unsigned)n * 4u : 0x80000000u;
+#pragma unroll
+    for (int t = 0; t < NSM; ++t) {
+      als[t] = 0.f;
+      if (NSC > 0 || t < NS) {
+        const __amdgpu_buffer_rsrc_t rA =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(alb + (long long)t * N), (short)0, N * 4, 0x00020000);
+        als[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rA, off, 0, 0));
+      }
+    }
+  }
+  // Long-range rows, one ring of PF slots for both passes: pass 1 takes the V rows of taps
+  // 0..NS-1 (slot t % PF), pass 2 the K rows (tap t in slot (NS + t) % PF).  Rows n0w - delta
+  // + 0..15, whole rows per D/8 lanes.
+  uint4 rS[PF][CHW];
+  auto load_rows = [&](int k) {  // k-th block of the combined sequence V(0..NS-1), K(0..NS-1)
+    const bool isv = k < NS;
+    const int m0 = n0w - dl_s[isv ? k : k - NS];
+#pragma unroll
+    for (int u = 0; u < CHW; ++u)
+      rS[k % PF][u] = isv ? bload16(rV, m0 * vsn + vlaneR[u]) : bload16(rK, m0 * ksn + klaneR[u]);
+  };
+#pragma unroll
+  for (int k = 0; k < PF; ++k)
+    if (k < 2 * NS) load_rows(k);
+
+  if (!HAS_SE && tid < J) {
+    sBias2[tid] = bias_ld * kLog2e;
+    sGain[tid] = gain_ld;
+  }
+#pragma unroll
+  for (int u = 0; u < CWIN; ++u) {
+    const int ci = tid + u * kBlock;
+    if (ci < WIN * CPS) {
+      st16(sK + (ci / CPS) * RV + (ci % CPS) * 8, wk[u]);
+      st16(sV + (ci / CPS) * RV + (ci % CPS) * 8, wv[u]);
+    }
+  }
+  __syncthreads();
+
+  // ---- 1. Dense band: S^T = K Q^T, U^T = V dOut^T. ----
+  f32x4_t accS[3], accU[3];
+#pragma unroll
+  for (int kk = 0; kk < 3; ++kk) {
+    accS[kk] = zero4();
+    accU[kk] = zero4();
+    const bf16_t* kr = sK + (16 * w + 16 * kk + i) * RV + 8 * g;
+    const bf16_t* vr = sV + (16 * w + 16 * kk + i) * RV + 8 * g;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
+      accU[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(vr + 32 * s)), oB[s], accU[kk]);
+    }
+  }
+  if constexpr (HAS_SE) {
+#pragma unroll
+    for (int jb = 0; jb < 3; ++jb) {
+      if (16 * jb > W) continue;
+      f32x4_t acc = zero4();
+      const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
+      const bf16_t* srl = sSElo + (16 * jb + i) * RV + 8 * g;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
+        acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(srl + 32 * s)), qB[s], acc);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * jb + 4 * g + r;
+        if (j <= W) sTw[i * TST + j] = fmaf(c2, acc[r], sBias2[j]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // Dense weights and u; D' collects alpha u of every tap of this lane's query column.
+  float al[12], uu[12];
+  float dlane = 0.f;
+  const int dl0 = 32 - 4 * g + i;
+  const float lse2 = row_ok ? lse_ld * kLog2e : 0.f;
+#pragma unroll
+  for (int kk = 0; kk < 3; ++kk) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int dl = dl0 - 16 * kk - r;
+      const bool ok = row_ok && (unsigned)dl <= (unsigned)W && n >= dl;
+      const int j = ok ? dl : 0;
+      const float s2 = fmaf(sGain[j] * c2, accS[kk][r], HAS_SE ? sTw[i * TST + j] : sBias2[j]);
+      const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
+      al[4 * kk + r] = alpha;
+      uu[4 * kk + r] = accU[kk][r];
+      dlane = fmaf(alpha, accU[kk][r], dlane);
+      // c q.k for dg goes to the table now (frees the score registers).
+      if (g_grad && (unsigned)dl <= (unsigned)W) sRAWw[i * TS + dl] = c * accS[kk][r];
+    }
+  }
+  if constexpr (TBL_IN_V) {
+    __syncthreads();  // every wave's band reads of sV are done: the tables move in
+    for (int j = J + g; j < 48; j += 4) sDSw[i * TS + j] = 0.f;
+  }
+
+  // ---- 2. Long-range pass 1: u_j = dOut . v_j of each row, into the table (no wait per tap). ----
+#pragma unroll
+  for (int t = 0; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        const float uv = group_sum<CPRP>(dot8_bf16(oR[u], rS[t % PF][u], 0.f));
+        if (rc_chunk<D>(l, u) == 0) sDSw[rc_row<D>(l, u) * TS + W + 1 + t] = uv;
+      }
+      if (t + PF < 2 * NS) load_rows(t + PF);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): every row's u is in the table
+  __builtin_amdgcn_wave_barrier();
+  float uus[NSM];
+#pragma unroll
+  for (int t = 0; t < NSM; ++t) {
+    uus[t] = 0.f;
+    if (NSC > 0 || t < NS) {
+      uus[t] = sDSw[i * TS + W + 1 + t];
+      dlane = fmaf(als[t], uus[t], dlane);  // als[t] is zero off the diagonal
+    }
+  }
+  const float Dp = col_sum(dlane);  // D' = dOut . o (pre-gain o) for query n
+
+  // ---- 3. dq = X + SE^T (c dS)^T, X = sum_j (c g_j dS_j) k_j. ----
+  f32x4_t X[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) X[db] = zero4();
+  const float ca = c * a;
+#pragma unroll
+  for (int kk = 0; kk < 3; ++kk) {
+    float wq[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int dl = dl0 - 16 * kk - r;
+      const bool in = (unsigned)dl <= (unsigned)W;
+      const int j = in ? dl : 0;
+      const float du = al[4 * kk + r] * (uu[4 * kk + r] - Dp);
+      if (in) sDSw[i * TS + dl] = a * du;  // every entry j <= W is written (zero where masked)
+      wq[r] = sGain[j] * ca * du;
+    }
+    // The weights as bf16 hi + lo pairs: the products keep the weights' fp32 precision.
+    s16x4_t bw, bwl;
+    split_bf16x4(wq[0], wq[1], wq[2], wq[3], bw, bwl);
+    const bf16_t* kr = sK + (16 * w + 16 * kk + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const s16x4_t at = lds_read_tr16(kr + 16 * db);
+      X[db] = mfma_16x16x16(at, bw, X[db]);
+      X[db] = mfma_16x16x16(at, bwl, X[db]);
+    }
+  }
+
+  // Long-range pass 2 (diagonal of one 16x16 tile per tap): the tap's key rows are staged in
+  // the wave's block (natural row order) for the transposing reads.
+  unsigned* const lw = reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N + n;
+  const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+#pragma unroll
+  for (int t = 0; t < NSM; ++t) {
+    if (NSC > 0 || t < NS) {
+      const int j = W + 1 + t;
+      const int slot = (NS + t) % PF;
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, rS[slot][u]);
+        if constexpr (DG) {
+          const float qk = group_sum<CPRP>(dot8_bf16(qR[u], rS[slot][u], 0.f));
+          if (rc_chunk<D>(l, u) == 0) sRAWw[rc_row<D>(l, u) * TS + j] = c * qk;
+        }
+      }
+      if (NS + t + PF < 2 * NS) load_rows(NS + t + PF);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
+      __builtin_amdgcn_wave_barrier();
+      const float ds = a * als[t] * (uus[t] - Dp);  // zero off the diagonal and for masked taps
+      const float wq = c * sGain[j] * ds;
+      if (diag) {
+        sDSw[i * TS + j] = ds;
+        if (row_ok) lw[(long long)t * N] = cvt_pk_bf16(wq, a * als[t]);
+      }
+      s16x4_t bw, bwl;
+      split_onehot_bf16x4(wq, i & 3, bw, bwl);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const s16x4_t at = lds_read_tr16(ksr + 16 * db);
+        X[db] = mfma_16x16x16(at, bw, X[db]);
+        X[db] = mfma_16x16x16(at, bwl, X[db]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  if constexpr (HAS_SE) {
+    // The wave's Q rows (natural order) replace its K rows, for dse once every table is done.
+    if (se_grad) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last tap's transposed reads are done
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int u = 0; u < CHW; ++u)
+        if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
+    }
+  }
+  if (g == 0) sDp[w][i] = row_ok ? Dp : 0.f;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+
+  // dbias / dg column sums of this wave's 16 table rows (its own writes, complete above),
+  // and the wave's sum of D' (for da).
   float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
+  if (l < J) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float ds = sDSw[r * TS + l];
+      acc_bias += ds;
+      if (g_grad) acc_gain = fmaf(ds, sRAWw[r * TS + l], acc_gain);
+    }
+  }
+  if (l == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc_if += sDp[w][r];
+  }
+
   f32x4_t accSE[HAS_SE ? TPW : 1];  // this wave's dse^T tiles w, w+4, ...
 #pragma unroll
   for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
-
-  float* sDSw = sDS + w * 16 * TS;
-  float* sRAWw = sRAW + w * 16 * TS;  // dereferenced only when g_grad
-  // The wave's 16 values of D' go through its own hand-off block once the tap loop is over.
-  float* sDpw = &sPair[w][0][0];
-  bf16_t* sKsw = sKs[w];
-  float* sTw = reinterpret_cast<float*>(sKsw);
-  const int t_begin = chunk * p.tiles_per_block;
-  // Without scale_embed the plan gives one tile per workgroup (checked at launch): a loop of
-  // one trip keeps the compiler from holding loop-invariant addresses across tiles.
-  const int t_end = t_begin + 1;
-  int dl_s[NSM];
-  load_sparse_deltas(p.taps, dl_s);
-
-  for (int tile = t_begin; tile < t_end; ++tile) {
-    const int n0 = tile * QT;
-    const int n0w = n0 + 16 * w;
-    const int n = n0w + i;
-    const bool row_ok = n < N;
-
-    // ---- Loads (zero outside [0, N)). ----
-    // Dense window K and V rows [n0-32, n0+64), staged once per workgroup in LDS.
-    uint4 wk[CWIN], wv[CWIN];
+  if constexpr (HAS_SE) {
+    // SE^T (c dS)^T from this wave's own table rows: dq's scale_embed term.
 #pragma unroll
-    for (int u = 0; u < CWIN; ++u) {
-      const int ci = tid + u * kBlock;
-      const bool cv = ci % CPS < CPR;
-      wk[u] = bload16(rK, (n0 - kMaxWindow) * ksn + opaque(cv ? (ci / CPS) * ksn + (ci % CPS) * 8 : kNoElem));
-      wv[u] = bload16(rV, (n0 - kMaxWindow) * vsn + opaque(cv ? (ci / CPS) * vsn + (ci % CPS) * 8 : kNoElem));
-    }
-    if constexpr (!HAS_SE) {
-      bias_ld = p.pos_bias[jc * p.H + h];
-      gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
-    }
-    bf16x8_t qB[KS], oB[KS];
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const bool sv = 8 * g + 32 * s < D;  // the zero columns of D = 80's last K-step
-      qB[s] = as_bf16x8(bload16(rQ, n0w * qsn + (sv ? qlane + 32 * s : kNoElem)));
-      oB[s] = as_bf16x8(bload16(rO, n0w * dosn + (sv ? olane + 32 * s : kNoElem)));
-    }
-    uint4 qR[CHW], oR[CHW];
-#pragma unroll
-    for (int u = 0; u < CHW; ++u) {
-      qR[u] = bload16(rQ, n0w * qsn + qlaneR[u]);
-      oR[u] = bload16(rO, n0w * dosn + olaneR[u]);
-    }
-    // Unconditional (a row past N reads row N - 1 and is masked below): a load under the row
-    // test was waited for inside the branch, before the long-range loads could be issued.
-    const float lse_ld = p.lse[rowbase + (row_ok ? n : N - 1)];
-    // Long-range K/V rows n0w - delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
-    uint4 kS[PF][CHW], vS[PF][CHW];
-#pragma unroll
-    for (int t = 0; t < PF; ++t) {
-      if (t < NS) {
-        const int m0 = n0w - dl_s[t];
-#pragma unroll
-        for (int u = 0; u < CHW; ++u) {
-          kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
-          vS[t][u] = bload16(rV, m0 * vsn + vlaneR[u]);
-        }
-      }
-    }
-
-    if (!HAS_SE && tid < J) {
-      sBias2[tid] = bias_ld * kLog2e;
-      sGain[tid] = gain_ld;
-    }
-
-    __syncthreads();  // previous tile's readers of sK / tables are done
-#pragma unroll
-    for (int u = 0; u < CWIN; ++u) {
-      const int ci = tid + u * kBlock;
-      if (ci < WIN * CPS) {
-        st16(sK + (ci / CPS) * RV + (ci % CPS) * 8, wk[u]);
-        st16(sV + (ci / CPS) * RV + (ci % CPS) * 8, wv[u]);
-      }
-    }
-    __syncthreads();
-
-    // ---- Dense band: S^T = K Q^T, U^T = V dOut^T. ----
-    f32x4_t accS[3], accU[3];
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-      accS[kk] = zero4();
-      accU[kk] = zero4();
-      const bf16_t* kr = sK + (16 * w + 16 * kk + i) * RV + 8 * g;
-      const bf16_t* vr = sV + (16 * w + 16 * kk + i) * RV + 8 * g;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
-        accU[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(vr + 32 * s)), oB[s], accU[kk]);
-      }
-    }
-    if constexpr (HAS_SE) {
-#pragma unroll
-      for (int jb = 0; jb < 3; ++jb) {
-        f32x4_t acc = zero4();
-        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
-        const bf16_t* srl = sSElo + (16 * jb + i) * RV + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
-          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(srl + 32 * s)), qB[s], acc);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * jb + 4 * g + r;
-          if (j <= W) sTw[i * TST + j] = fmaf(c2, acc[r], sBias2[j]);
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);
-      __builtin_amdgcn_wave_barrier();
-    }
-
-    // Dense weights first; D0 = the band's weighted mean of u is subtracted from u before the
-    // bf16 rounding of the dQ operands, so their error scales with u - D' rather than u.
-    float al[12], uu[12];
-    float dlane = 0.f, wlane = 0.f;
-    const int dl0 = 32 - 4 * g + i;
-    const float lse2 = row_ok ? lse_ld * kLog2e : 0.f;
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int dl = dl0 - 16 * kk - r;
-        const bool ok = row_ok && (unsigned)dl <= (unsigned)W && n >= dl;
-        const int j = ok ? dl : 0;
-        const float s2 = fmaf(sGain[j] * c2, accS[kk][r], HAS_SE ? sTw[i * TST + j] : sBias2[j]);
-        const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
-        al[4 * kk + r] = alpha;
-        uu[4 * kk + r] = accU[kk][r];
-        dlane = fmaf(alpha, accU[kk][r], dlane);
-        wlane += alpha;
-        // c q.k for dg goes to the table now (frees the score registers for the taps loop).
-        if (g_grad && (unsigned)dl <= (unsigned)W) sRAWw[i * TS + dl] = c * accS[kk][r];
-      }
-    }
-    const float wsum = col_sum(wlane);
-    const float D0 = wsum > 0.f ? col_sum(dlane) / wsum : 0.f;
-    if constexpr (TBL_IN_V) {
-      __syncthreads();  // every wave's band reads of sV are done: the dS tables move in
-      for (int j = J + g; j < 48; j += 4) sDSw[i * TS + j] = 0.f;
-    }
-    if constexpr (HAS_SE) {
-      // T for the long-range taps (log2e (bias_j + c q.se_j), the same MFMA as the dense taps'
-      // table) waits in the taps' dS table slots until the diagonal lane reads it in the taps
-      // loop; dS overwrites it after the loop.
-#pragma unroll
-      for (int jb = 0; jb < 3; ++jb) {
-        if (16 * jb + 15 <= W) continue;
-        f32x4_t acc = zero4();
-        const bf16_t* sr = sSE + (16 * jb + i) * RV + 8 * g;
-        const bf16_t* srl = sSElo + (16 * jb + i) * RV + 8 * g;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(sr + 32 * s)), qB[s], acc);
-          acc = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(srl + 32 * s)), qB[s], acc);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * jb + 4 * g + r;
-          if (j > W && j < J) sDSw[i * TS + j] = fmaf(c2, acc[r], sBias2[j]);
-        }
-      }
-    }
-    f32x4_t X[DB], Y[DB];
-#pragma unroll
-    for (int db = 0; db < DB; ++db) { X[db] = zero4(); Y[db] = zero4(); }
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk) {
-      float ga[4], gau[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int dl = dl0 - 16 * kk - r;
-        const int j = (unsigned)dl <= (unsigned)W ? dl : 0;
-        ga[r] = sGain[j] * al[4 * kk + r];
-        gau[r] = ga[r] * (uu[4 * kk + r] - D0);
-      }
-      // The weights as bf16 hi + lo pairs: the products keep the weights' fp32 precision.
-      s16x4_t b1, b1l, b2, b2l;
-      split_bf16x4(gau[0], gau[1], gau[2], gau[3], b1, b1l);
-      split_bf16x4(ga[0], ga[1], ga[2], ga[3], b2, b2l);
-      const bf16_t* kr = sK + (16 * w + 16 * kk + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
+    for (int jb = 0; jb < 3; ++jb) {
+      const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
+      s16x4_t bs, bsl;
+      split_bf16x4(c * d4.x, c * d4.y, c * d4.z, c * d4.w, bs, bsl);
+      const int so = (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const s16x4_t at = lds_read_tr16(kr + 16 * db);
-        X[db] = mfma_16x16x16(at, b1, X[db]);
-        X[db] = mfma_16x16x16(at, b1l, X[db]);
-        Y[db] = mfma_16x16x16(at, b2, Y[db]);
-        Y[db] = mfma_16x16x16(at, b2l, Y[db]);
+        const s16x4_t sh = lds_read_tr16(sSE + so + 16 * db);
+        X[db] = mfma_16x16x16(sh, bs, X[db]);
+        X[db] = mfma_16x16x16(sh, bsl, X[db]);
+        X[db] = mfma_16x16x16(lds_read_tr16(sSElo + so + 16 * db), bs, X[db]);
       }
     }
-
-    // ---- Long-range taps (diagonal of one 16x16 tile each). ----
-    const bool diag = g == (i >> 2);
-    const uint2 ohm = onehot_masks(i & 3);
-    const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
-    float als[NSM], uus[NSM];
-#pragma unroll
-    for (int t = 0; t < NSM; ++t) {
-      als[t] = 0.f; uus[t] = 0.f;
-      if (NSC > 0 || t < NS) {
-        const int j = W + 1 + t;
-        // q.k and dOut.v on the VALU: each lane dots its 16-byte chunk, the row's lanes sum
-        // (DPP), and one lane per row hands the results to the diagonal lane through LDS.  The
-        // key rows are staged (natural row order) for the transposing reads of X and Y.
-#pragma unroll
-        for (int u = 0; u < CHW; ++u) {
-          const float qk = group_sum<CPRP>(dot8_bf16(qR[u], kS[t % PF][u], 0.f));
-          const float dv = group_sum<CPRP>(dot8_bf16(oR[u], vS[t % PF][u], 0.f));
-          if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, kS[t % PF][u]);
-          if (rc_chunk<D>(l, u) == 0)
-            *reinterpret_cast<float2*>(sPair[w][rc_row<D>(l, u)]) = float2{qk, dv};
-        }
-        if (t + PF < NS) {
-          const int m0 = n0w - dl_s[t + PF];
-#pragma unroll
-          for (int u = 0; u < CHW; ++u) {
-            kS[t % PF][u] = bload16(rK, m0 * ksn + klaneR[u]);
-            vS[t % PF][u] = bload16(rV, m0 * vsn + vlaneR[u]);
-          }
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): staged rows and pairs are written
-        __builtin_amdgcn_wave_barrier();
-        const float2 pr = *reinterpret_cast<const float2*>(sPair[w][i]);
-        const float raw = pr.x, uval = pr.y;
-        const float s2 = fmaf(sGain[j] * c2, raw, HAS_SE ? sDSw[i * TS + j] : sBias2[j]);
-        const bool ok = diag && row_ok && n >= dl_s[t];
-        const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lse2) : 0.f;
-        als[t] = alpha;
-        uus[t] = uval;
-        if (g_grad && diag) sRAWw[i * TS + j] = c * raw;
-        dlane = fmaf(alpha, uval, dlane);
-        const float gal = sGain[j] * alpha;
-        // One-hot weights as bf16 hi + lo pairs: the products keep the weights' fp32 precision.
-        s16x4_t b1, b1l, b2, b2l;
-        // With scale_embed they are placed by per-lane element masks (fewer instructions; that
-        // variant then fits without spills), without by 64-bit shifts (no extra registers).
-        if constexpr (HAS_SE) {
-          split_onehot_bf16x4(gal * (uval - D0), ohm, b1, b1l);
-          split_onehot_bf16x4(gal, ohm, b2, b2l);
-        } else {
-          split_onehot_bf16x4(gal * (uval - D0), i & 3, b1, b1l);
-          split_onehot_bf16x4(gal, i & 3, b2, b2l);
-        }
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const s16x4_t at = lds_read_tr16(ksr + 16 * db);
-          X[db] = mfma_16x16x16(at, b1, X[db]);
-          X[db] = mfma_16x16x16(at, b1l, X[db]);
-          Y[db] = mfma_16x16x16(at, b2, Y[db]);
-          Y[db] = mfma_16x16x16(at, b2l, Y[db]);
-        }
-      }
-    }
-
-    const float Dp = col_sum(dlane);  // D' = dOut . o (pre-gain o) for query n
-    if constexpr (HAS_SE) {
-      // The wave's Q rows (natural order) replace its K rows, for dse after the tables are done.
-      if (se_grad) {
-#pragma unroll
-        for (int u = 0; u < CHW; ++u)
-          if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
-      }
-    }
-
-    // ---- dS table [query][tap] (every entry j < J is written: zero where masked). ----
-#pragma unroll
-    for (int kk = 0; kk < 3; ++kk)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int dl = dl0 - 16 * kk - r;
-        if ((unsigned)dl <= (unsigned)W) {
-          const float dS = a * al[4 * kk + r] * (uu[4 * kk + r] - Dp);
-          sDSw[i * TS + dl] = dS;
-        }
-      }
-    if (diag) {
-      // The long-range taps' dk/dv weights go to the workspace for launch 2, which then needs
-      // neither the taps' dot products nor their queries' lse and D': [b,h][tap][query] dwords
-      // holding bf16(c g_j dS_j) (low half) and bf16(a alpha_j) (high half), zero for a masked tap.
-      unsigned* const lw = reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N + n;
-#pragma unroll
-      for (int t = 0; t < NSM; ++t)
-        if (NSC > 0 || t < NS) {
-          const float ds = a * als[t] * (uus[t] - Dp);
-          sDSw[i * TS + W + 1 + t] = ds;
-          if (row_ok) lw[(long long)t * N] = cvt_pk_bf16(c * sGain[W + 1 + t] * ds, a * als[t]);
-        }
-    }
-    if (g == 0) sDpw[i] = row_ok ? Dp : 0.f;
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-
-    // dq = c (a (X - D' Y) + SE^T dS^T): c a X - c a (D' - D0) Y, plus SE^T (c dS)^T.
-    f32x4_t dQ[DB];
-    const float ca = c * a, cad = ca * (Dp - D0);
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) dQ[db][r] = fmaf(ca, X[db][r], -cad * Y[db][r]);
-    if constexpr (HAS_SE) {
-#pragma unroll
-      for (int jb = 0; jb < 3; ++jb) {
-        const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
-        s16x4_t bs, bsl;
-        split_bf16x4(c * d4.x, c * d4.y, c * d4.z, c * d4.w, bs, bsl);
-        const int so = (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
-#pragma unroll
-        for (int db = 0; db < DB; ++db) {
-          const s16x4_t sh = lds_read_tr16(sSE + so + 16 * db);
-          dQ[db] = mfma_16x16x16(sh, bs, dQ[db]);
-          dQ[db] = mfma_16x16x16(sh, bsl, dQ[db]);
-          dQ[db] = mfma_16x16x16(lds_read_tr16(sSElo + so + 16 * db), bs, dQ[db]);
-        }
-      }
-    }
-    // dq (MFMA layout: lane (i, g) holds query i, d = 16 db + 4 g + 0..3) leaves as whole rows
-    // through a wave-private LDS block (the K staging block; with scale_embed it holds the Q
-    // rows for dse, and the wave's rows of the K window, free since the barrier after the band,
-    // take its place), then 16-byte row pieces per lane.  Without a free block (scale_embed at
-    // D = 32, whose tables stay outside the V window) the quads are stored directly.
-    if constexpr (!HAS_SE || TBL_IN_V) {
-      bf16_t* const stg = HAS_SE ? sK + 16 * w * RV : sKsw;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        *reinterpret_cast<uint2*>(stg + i * RV + 16 * db + 4 * g) =
-            pack_bf16x4_u2(dQ[db][0], dQ[db][1], dQ[db][2], dQ[db][3]);
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
-        if (n0w + rr < N && cc < CPR)
-          st16(dqb + (n0w + rr) * p.dqs.n + 8 * cc, *reinterpret_cast<const uint4*>(stg + rr * RV + 8 * cc));
-      }
-    } else if (row_ok) {
-      bf16_t* o = dqb + n * p.dqs.n + 4 * g;
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-        *reinterpret_cast<uint2*>(o + 16 * db) =
-            pack_bf16x4_u2(dQ[db][0], dQ[db][1], dQ[db][2], dQ[db][3]);
-    }
-    if (row_ok && g == 0) p.dpre[rowbase + n] = Dp;
-
-    // dbias / dg column sums of this wave's 16 table rows (its own writes, complete above),
-    // and the wave's sum of D' (for da): no workgroup barrier inside the tile.
-    if (l < J) {
-      float sb = 0.f, sg = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float ds = sDSw[r * TS + l];
-        sb += ds;
-        if (g_grad) sg = fmaf(ds, sRAWw[r * TS + l], sg);
-      }
-      acc_bias += sb;
-      acc_gain += sg;
-    }
-    if (l == 0) {
-      float sa = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sa += sDpw[r];
-      acc_if += sa;
-    }
-    if constexpr (HAS_SE) __syncthreads();  // all waves' tables (and Q rows) are complete
+    __syncthreads();  // all waves' tables and Q rows are complete, all band reads of sK done
     // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j) over the tile's 64
     // queries; wave w owns the output tiles w, w+4, ... of the 3 x DB grid.
-    if constexpr (HAS_SE) {
-      if (se_grad) {
+    if (se_grad) {
 #pragma unroll
-        for (int k = 0; k < TPW; ++k) {
-          const int idx = w + 4 * k;
-          if (idx < NTSE) {
-            const int jb = idx / DB, db = idx - jb * DB;
+      for (int k = 0; k < TPW; ++k) {
+        const int idx = w + 4 * k;
+        if (idx < NTSE) {
+          const int jb = idx / DB, db = idx - jb * DB;
 #pragma unroll
-            for (int ww = 0; ww < 4; ++ww) {
-              const float* col = sDS + (ww * 16 + 4 * g) * TS + 16 * jb + i;
-              s16x4_t bs, bsl;
-              split_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS], bs, bsl);
-              const bf16_t* qr = sKs[ww] + (4 * g + (i >> 2)) * RV + 4 * (i & 3) + 16 * db;
-              const s16x4_t qt = lds_read_tr16(qr);
-              accSE[k] = mfma_16x16x16(qt, bs, accSE[k]);
-              accSE[k] = mfma_16x16x16(qt, bsl, accSE[k]);
-            }
+          for (int ww = 0; ww < 4; ++ww) {
+            const float* col = sDS + (ww * 16 + 4 * g) * TS + 16 * jb + i;
+            s16x4_t bs, bsl;
+            split_bf16x4(col[0], col[TS], col[2 * TS], col[3 * TS], bs, bsl);
+            const bf16_t* qr = sKs[ww] + (4 * g + (i >> 2)) * RV + 4 * (i & 3) + 16 * db;
+            const s16x4_t qt = lds_read_tr16(qr);
+            accSE[k] = mfma_16x16x16(qt, bs, accSE[k]);
+            accSE[k] = mfma_16x16x16(qt, bsl, accSE[k]);
           }
         }
       }
     }
   }
 
+  // dq (MFMA layout: lane (i, g) holds query i, d = 16 db + 4 g + 0..3) leaves as whole rows
+  // through a wave-private LDS block: the K staging block, or with scale_embed (whose staging
+  // block holds the Q rows for dse) the wave's rows of the K window, free after the barrier
+  // above.  Without such a block (scale_embed at D = 32, whose tables stay outside the V window)
+  // the quads are stored directly.
+  if constexpr (!HAS_SE || TBL_IN_V) {
+    if constexpr (!HAS_SE) {
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last tap's transposed reads are done
+      __builtin_amdgcn_wave_barrier();
+    }
+    bf16_t* const stg = HAS_SE ? sK + 16 * w * RV : sKsw;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      *reinterpret_cast<uint2*>(stg + i * RV + 16 * db + 4 * g) =
+          pack_bf16x4_u2(X[db][0], X[db][1], X[db][2], X[db][3]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < CHW; ++u) {
+      const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+      if (n0w + rr < N && cc < CPR)
+        st16(dqb + (n0w + rr) * p.dqs.n + 8 * cc, *reinterpret_cast<const uint4*>(stg + rr * RV + 8 * cc));
+    }
+  } else if (row_ok) {
+    bf16_t* o = dqb + n * p.dqs.n + 4 * g;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      *reinterpret_cast<uint2*>(o + 16 * db) = pack_bf16x4_u2(X[db][0], X[db][1], X[db][2], X[db][3]);
+  }
+  if (row_ok && g == 0) p.dpre[rowbase + n] = Dp;
+
   // The four waves' partial sums meet in their own (now free) table blocks; one partial row per
   // workgroup, summed in wave order.
   {
-    if constexpr (HAS_SE) __syncthreads();  // the last tile's dse reads of every wave's table are done
+    __syncthreads();  // every wave's reads of the tables (column sums, dse, SE term) are done
     float* red = sDSw;  // wave-private until the barrier
     if (l < J) { red[l] = acc_bias; red[64 + l] = acc_gain; }
     if (l == 0) red[128] = acc_if;
@@ -614,7 +571,7 @@ static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
 template <int D>
 static hipError_t launch_dq_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
   // The scale_embed variant also serves dse requested at se = 0.
-  if (p.tiles_per_block != 1) return hipErrorInvalidValue;  // the single-tile form
+  if (p.tiles_per_block != 1) return hipErrorInvalidValue;  // one tile per workgroup
   if (p.scale_embed || p.part_se) launch_dq_mfma_ns<D, true>(p, nb, st);
   else launch_dq_mfma_ns<D, false>(p, nb, st);
   return hipGetLastError();

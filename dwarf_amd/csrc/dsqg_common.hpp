@@ -136,6 +136,9 @@ struct FwdParams {
   const float* if_gain;      // [H] or null
   void* out; Strides4 os;
   float* lse;                // [B,H,N] or null
+  // bf16: the long-range taps' softmax weights alpha_j (pre-gain), [B,H,NS,N] fp32 with
+  // NS = J - W - 1 taps beyond the dense window, or null (not written).
+  float* alpha_lr;
 };
 
 struct ReduceParams {
@@ -160,6 +163,7 @@ struct BwdParams {
   const void* v; Strides4 vs;
   const void* dout; Strides4 dos;
   const float* lse;
+  const float* alpha_lr;  // bf16: the forward's long-range weights [B,H,NS,N] (FwdParams::alpha_lr)
   const float* pos_bias;
   const float* scale_embed;
   const float* score_gain;

@@ -21,6 +21,8 @@
 //  5. Softmax over each query's J taps in registers: the four lanes of a query column combine
 //     max and sum with two cross-lane steps; lse = max + log(sum); the weights are normalised
 //     (and scaled by the IF gain) before P V.
+//     With an alpha_lr buffer the long-range taps' normalised weights are also stored, for the
+//     backward ([b,h][tap][query] fp32).
 //  6. P V: O^T = V^T P^T with v_mfma_f32_16x16x16_bf16.  Dense taps: V^T from the row-major
 //     window tile through ds_read_tr16_b64, P^T already in B layout.  Long-range taps: each
 //     tap's 16 V rows (gathered whole-row) are staged in the wave's LDS block and read back the
@@ -324,6 +326,15 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   const long long rowbase = ((long long)b * p.H + h) * N;
   if (row_ok && g == 0 && p.lse) p.lse[rowbase + n] = (mx + __log2f(lsum)) * 0.6931471805599453f;
   const float inv = row_ok ? if_a / lsum : 0.f;
+  // The long-range taps' weights alpha_j = e_j / sum (zero where masked) for the backward, which
+  // then recomputes no long-range score: [b,h][tap][query], written by the query's diagonal lane.
+  if (p.alpha_lr && diag && row_ok) {
+    float* const alw = p.alpha_lr + ((long long)(b * p.H + h) * NS) * N + n;
+    const float rl = 1.0f / lsum;
+#pragma unroll
+    for (int t = 0; t < NSM; ++t)
+      if (NSC > 0 || t < NS) alw[(long long)t * N] = ss[t] * rl;
+  }
 
   // ---- Dense P V: O^T = V^T P^T. ----
   f32x4_t accO[DB];

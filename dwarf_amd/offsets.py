@@ -34,3 +34,14 @@ def validate(offsets) -> tuple:
     if not offs or offs[0] != 0 or any(b <= a for a, b in zip(offs, offs[1:])):
         raise AssertionError(f"offsets must be strictly increasing and start at 0: {offs}")
     return offs
+
+
+def long_range_taps(offsets) -> int:
+    """Taps beyond the dense window: the table's leading run 0, 1, ..., W (W <= 32) is the
+    window the kernels stage whole; the rest (NS = J - W - 1) are gathered row blocks, whose
+    softmax weights the bf16 forward saves for the backward ([B,H,NS,N])."""
+    offs = tuple(int(o) for o in offsets)
+    W = 0
+    while W + 1 < len(offs) and W + 1 <= 32 and offs[W + 1] == W + 1:
+        W += 1
+    return len(offs) - W - 1

@@ -21,6 +21,7 @@ import torch
 from torch import Tensor
 
 from . import _lib
+from .offsets import long_range_taps
 
 _DTYPE_CODE = {torch.float32: _lib.DSQG_F32, torch.bfloat16: _lib.DSQG_BF16}
 
@@ -103,6 +104,9 @@ class FwdLaunch:
         pb, se, sg, ig = _param(pos_bias), _param(scale_embed), _param(score_gain), _param(if_gain)
         self.out = _token_major(B, H, N, D, dtype=q.dtype, device=dev)
         self.lse = torch.empty((B, H, N), dtype=torch.float32, device=dev)
+        # bf16: the long-range taps' weights, saved for the backward (which needs them).
+        self.alpha_lr = torch.empty(_alpha_shape(q.dtype, B, H, N, offsets), dtype=torch.float32,
+                                    device=dev)
         self._keep = (q, k, v, pb, se, sg, ig)
         a = _lib.FwdArgs()
         a.shape = _lib.make_shape(code, B, H, N, D, offsets)
@@ -112,38 +116,47 @@ class FwdLaunch:
         a.pos_bias, a.scale_embed, a.score_gain, a.if_gain = _ptr(pb), _ptr(se), _ptr(sg), _ptr(ig)
         a.out, a.out_stride = _ptr(self.out), _strides(self.out)
         a.lse = _ptr(self.lse)
+        a.alpha_lr = _ptr(self.alpha_lr)
         self.args = a
 
     def run(self) -> None:
         _lib.check(self.lib.dsqg_fwd(ctypes.byref(self.args), _stream(self.device)), "dsqg_fwd")
 
 
+def _alpha_shape(dtype, B: int, H: int, N: int, offsets) -> tuple:
+    """Shape of the forward's saved long-range weights: [B,H,NS,N] for bf16, empty for fp32."""
+    ns = long_range_taps(offsets)
+    return (B, H, ns, N) if dtype == torch.bfloat16 and ns > 0 else (0,)
+
+
 @torch.library.custom_op("dwarf::dsqg_fwd", mutates_args=())
 def dsqg_fwd(q: Tensor, k: Tensor, v: Tensor, pos_bias: Tensor,
              scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
-             if_gain: Optional[Tensor], offsets: List[int]) -> Tuple[Tensor, Tensor]:
-    """out [B,H,N,D] (dtype of q; token-major storage) and lse [B,H,N] fp32."""
+             if_gain: Optional[Tensor], offsets: List[int]) -> Tuple[Tensor, Tensor, Tensor]:
+    """out [B,H,N,D] (dtype of q; token-major storage), lse [B,H,N] fp32 and (bf16) the
+    long-range taps' weights alpha_lr [B,H,NS,N] fp32 for the backward (empty for fp32)."""
     launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
     launch.run()
-    return launch.out, launch.lse
+    return launch.out, launch.lse, launch.alpha_lr
 
 
 @dsqg_fwd.register_fake
 def _(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
     B, H, N, D = q.shape
-    return q.new_empty((B, N, H, D)).permute(0, 2, 1, 3), q.new_empty((B, H, N), dtype=torch.float32)
+    return (q.new_empty((B, N, H, D)).permute(0, 2, 1, 3), q.new_empty((B, H, N), dtype=torch.float32),
+            q.new_empty(_alpha_shape(q.dtype, B, H, N, offsets), dtype=torch.float32))
 
 
 @torch.library.custom_op("dwarf::dsqg_fwd_qkv", mutates_args=())
 def dsqg_fwd_qkv(qkv: Tensor, num_heads: int, pos_bias: Tensor, scale_embed: Optional[Tensor],
                  score_gain: Optional[Tensor], if_gain: Optional[Tensor],
-                 offsets: List[int]) -> Tuple[Tensor, Tensor]:
+                 offsets: List[int]) -> Tuple[Tensor, Tensor, Tensor]:
     """dsqg_fwd on the q, k, v head views of one projection output qkv [B,N,3*H*HD]; its
     gradient is returned as one [B,N,3*H*HD] tensor (no per-head concatenation)."""
     q, k, v = split_qkv(qkv, num_heads)
     launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
     launch.run()
-    return launch.out, launch.lse
+    return launch.out, launch.lse, launch.alpha_lr
 
 
 @dsqg_fwd_qkv.register_fake
@@ -151,7 +164,8 @@ def _(qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets):
     B, N, E3 = qkv.shape
     HD = E3 // (3 * num_heads)
     return (qkv.new_empty((B, N, num_heads, HD)).permute(0, 2, 1, 3),
-            qkv.new_empty((B, num_heads, N), dtype=torch.float32))
+            qkv.new_empty((B, num_heads, N), dtype=torch.float32),
+            qkv.new_empty(_alpha_shape(qkv.dtype, B, num_heads, N, offsets), dtype=torch.float32))
 
 
 # ------------------------------------------------------------------------------------------
@@ -169,7 +183,7 @@ class BwdLaunch:
               "params": "dsqg_bwd_params"}
 
     def __init__(self, q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
-                 need_dse, need_dg, need_da, grads=None):
+                 need_dse, need_dg, need_da, grads=None, alpha_lr=None):
         dev = _require_gpu(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain)
         self.lib = _lib.load()
         self.device = dev
@@ -181,6 +195,8 @@ class BwdLaunch:
                                  f"{q.dtype}/{dout.dtype}")
         q, k, v, dout = _rows_ready(q), _rows_ready(k), _rows_ready(v), _rows_ready(dout)
         lse = lse.contiguous()
+        if alpha_lr is not None:  # the forward's long-range weights (bf16), [B,H,NS,N] fp32
+            alpha_lr = alpha_lr.contiguous()
         pb, se, sg, ig = _param(pos_bias), _param(scale_embed), _param(score_gain), _param(if_gain)
         if grads is None:  # else (dq, dk, dv) [B,H,N,D] views the caller allocated
             grads = tuple(torch.empty((B, H, N, D), dtype=q.dtype, device=dev) for _ in range(3))
@@ -190,7 +206,7 @@ class BwdLaunch:
         self.dscale_embed = torch.empty((J, D) if need_dse else (0,), **f32)
         self.dscore_gain = torch.empty((H, J) if need_dg else (0,), **f32)
         self.dif_gain = torch.empty((H,) if need_da else (0,), **f32)
-        self._keep = (q, k, v, dout, lse, pb, se, sg, ig)
+        self._keep = (q, k, v, dout, lse, alpha_lr, pb, se, sg, ig)
         a = _lib.BwdArgs()
         a.shape = _lib.make_shape(code, B, H, N, D, offsets)
         a.q, a.q_stride = _ptr(q), _strides(q)
@@ -198,6 +214,7 @@ class BwdLaunch:
         a.v, a.v_stride = _ptr(v), _strides(v)
         a.dout, a.dout_stride = _ptr(dout), _strides(dout)
         a.lse = _ptr(lse)
+        a.alpha_lr = _ptr(alpha_lr)
         a.pos_bias, a.scale_embed, a.score_gain, a.if_gain = _ptr(pb), _ptr(se), _ptr(sg), _ptr(ig)
         a.dq, a.dq_stride = _ptr(self.dq), _strides(self.dq)
         a.dk, a.dk_stride = _ptr(self.dk), _strides(self.dk)
@@ -223,19 +240,20 @@ class BwdLaunch:
 
 
 @torch.library.custom_op("dwarf::dsqg_bwd", mutates_args=())
-def dsqg_bwd(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, lse: Tensor, pos_bias: Tensor,
-             scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
+def dsqg_bwd(q: Tensor, k: Tensor, v: Tensor, dout: Tensor, lse: Tensor, alpha_lr: Tensor,
+             pos_bias: Tensor, scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
              if_gain: Optional[Tensor], offsets: List[int], need_dse: bool, need_dg: bool,
              need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
-    """(dq, dk, dv, dpos_bias, dscale_embed, dscore_gain, dif_gain); unrequested ones are empty."""
+    """(dq, dk, dv, dpos_bias, dscale_embed, dscore_gain, dif_gain); unrequested ones are empty.
+    lse and alpha_lr are the forward's."""
     launch = BwdLaunch(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
-                       need_dse, need_dg, need_da)
+                       need_dse, need_dg, need_da, alpha_lr=alpha_lr)
     launch.run()
     return launch.outputs()
 
 
 @dsqg_bwd.register_fake
-def _(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets, need_dse,
+def _(q, k, v, dout, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain, offsets, need_dse,
       need_dg, need_da):
     B, H, N, D = q.shape
     J = len(offsets)
@@ -247,22 +265,22 @@ def _(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets, n
 
 def _setup_context(ctx, inputs, output):
     q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets = inputs
-    _, lse = output
-    ctx.save_for_backward(q, k, v, lse, pos_bias, scale_embed, score_gain, if_gain)
+    _, lse, alpha_lr = output
+    ctx.save_for_backward(q, k, v, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain)
     ctx.offsets = list(offsets)
-    ctx.mark_non_differentiable(lse)
+    ctx.mark_non_differentiable(lse, alpha_lr)
 
 
-def _backward(ctx, dout, _dlse, direct: bool = False):
-    q, k, v, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
+def _backward(ctx, dout, _dlse, _dalpha, direct: bool = False):
+    q, k, v, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_dse = bool(need[4]) and scale_embed is not None
     need_dg = bool(need[5]) and score_gain is not None
     need_da = bool(need[6]) and if_gain is not None
-    args = (q, k, v, dout.to(q.dtype), lse, pos_bias, scale_embed, score_gain, if_gain,
+    args = (q, k, v, dout.to(q.dtype), lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain,
             ctx.offsets, need_dse, need_dg, need_da)
     if direct:
-        launch = BwdLaunch(*args)
+        launch = BwdLaunch(*args[:5], *args[6:], alpha_lr=alpha_lr)
         launch.run()
         dq, dk, dv, dpb, dse, dg, da = launch.outputs()
     else:
@@ -278,21 +296,21 @@ torch.library.register_autograd("dwarf::dsqg_fwd", _backward, setup_context=_set
 
 def _setup_context_qkv(ctx, inputs, output):
     qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets = inputs
-    _, lse = output
-    ctx.save_for_backward(qkv, lse, pos_bias, scale_embed, score_gain, if_gain)
+    _, lse, alpha_lr = output
+    ctx.save_for_backward(qkv, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain)
     ctx.num_heads = num_heads
     ctx.offsets = list(offsets)
-    ctx.mark_non_differentiable(lse)
+    ctx.mark_non_differentiable(lse, alpha_lr)
 
 
-def _backward_qkv(ctx, dout, _dlse, direct: bool = False):
-    qkv, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
+def _backward_qkv(ctx, dout, _dlse, _dalpha, direct: bool = False):
+    qkv, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_dse = bool(need[3]) and scale_embed is not None
     need_dg = bool(need[4]) and score_gain is not None
     need_da = bool(need[5]) and if_gain is not None
-    args = (qkv, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias, scale_embed, score_gain,
-            if_gain, ctx.offsets, need_dse, need_dg, need_da)
+    args = (qkv, ctx.num_heads, dout.to(qkv.dtype), lse, alpha_lr, pos_bias, scale_embed,
+            score_gain, if_gain, ctx.offsets, need_dse, need_dg, need_da)
     bwd = _bwd_qkv_impl if direct else dsqg_bwd_qkv
     dqkv, dpb, dse, dg, da = bwd(*args)
     return (dqkv, None, dpb.to(pos_bias.dtype),
@@ -302,32 +320,33 @@ def _backward_qkv(ctx, dout, _dlse, direct: bool = False):
 
 
 @torch.library.custom_op("dwarf::dsqg_bwd_qkv", mutates_args=())
-def dsqg_bwd_qkv(qkv: Tensor, num_heads: int, dout: Tensor, lse: Tensor, pos_bias: Tensor,
-                 scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
+def dsqg_bwd_qkv(qkv: Tensor, num_heads: int, dout: Tensor, lse: Tensor, alpha_lr: Tensor,
+                 pos_bias: Tensor, scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
                  if_gain: Optional[Tensor], offsets: List[int], need_dse: bool, need_dg: bool,
                  need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(dqkv [B,N,3*H*HD], dpos_bias, dscale_embed, dscore_gain, dif_gain): dq, dk, dv are
     written straight into the head views of one gradient buffer."""
-    return _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain,
-                         offsets, need_dse, need_dg, need_da)
+    return _bwd_qkv_impl(qkv, num_heads, dout, lse, alpha_lr, pos_bias, scale_embed, score_gain,
+                         if_gain, offsets, need_dse, need_dg, need_da)
 
 
-def _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
-                  need_dse, need_dg, need_da, k_eff=None, v_eff=None):
+def _bwd_qkv_impl(qkv, num_heads, dout, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain,
+                  offsets, need_dse, need_dg, need_da, k_eff=None, v_eff=None):
     q, k, v = split_qkv(qkv, num_heads)
     if k_eff is not None:  # K/V with the injection added (dsqg_fwd_qkv_kv)
         k, v = k_eff, v_eff
     dqkv = torch.empty_like(qkv, memory_format=torch.contiguous_format)
     launch = BwdLaunch(q, k, v, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets,
-                       need_dse, need_dg, need_da, grads=split_qkv(dqkv, num_heads))
+                       need_dse, need_dg, need_da, grads=split_qkv(dqkv, num_heads),
+                       alpha_lr=alpha_lr)
     launch.run()
     _, _, _, dpb, dse, dg, da = launch.outputs()
     return dqkv, dpb, dse, dg, da
 
 
 @dsqg_bwd_qkv.register_fake
-def _(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain, offsets, need_dse,
-      need_dg, need_da):
+def _(qkv, num_heads, dout, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain, offsets,
+      need_dse, need_dg, need_da):
     B, N, E3 = qkv.shape
     HD = E3 // (3 * num_heads)
     J = len(offsets)
@@ -356,14 +375,14 @@ def _kv_eff(qkv: Tensor, k_delta: Tensor, v_delta: Tensor, num_heads: int):
 def dsqg_fwd_qkv_kv(qkv: Tensor, k_delta: Tensor, v_delta: Tensor, num_heads: int,
                     pos_bias: Tensor, scale_embed: Optional[Tensor], score_gain: Optional[Tensor],
                     if_gain: Optional[Tensor],
-                    offsets: List[int]) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
-    """(out, lse, k + k_delta, v + v_delta): dsqg_fwd on q = the query view of qkv and the
-    injected K/V (returned for the backward)."""
+                    offsets: List[int]) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(out, lse, alpha_lr, k + k_delta, v + v_delta): dsqg_fwd on q = the query view of qkv
+    and the injected K/V (returned for the backward)."""
     k_eff, v_eff = _kv_eff(qkv, k_delta, v_delta, num_heads)
     q = split_qkv(qkv, num_heads)[0]
     launch = FwdLaunch(q, k_eff, v_eff, pos_bias, scale_embed, score_gain, if_gain, offsets)
     launch.run()
-    return launch.out, launch.lse, k_eff, v_eff
+    return launch.out, launch.lse, launch.alpha_lr, k_eff, v_eff
 
 
 @dsqg_fwd_qkv_kv.register_fake
@@ -372,23 +391,24 @@ def _(qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed, score_gain, if_ga
     HD = E3 // (3 * num_heads)
     return (qkv.new_empty((B, N, num_heads, HD)).permute(0, 2, 1, 3),
             qkv.new_empty((B, num_heads, N), dtype=torch.float32),
+            qkv.new_empty(_alpha_shape(qkv.dtype, B, num_heads, N, offsets), dtype=torch.float32),
             qkv.new_empty((B, num_heads, N, HD)), qkv.new_empty((B, num_heads, N, HD)))
 
 
 @torch.library.custom_op("dwarf::dsqg_bwd_qkv_kv", mutates_args=())
 def dsqg_bwd_qkv_kv(qkv: Tensor, k_eff: Tensor, v_eff: Tensor, num_heads: int, dout: Tensor,
-                    lse: Tensor, pos_bias: Tensor, scale_embed: Optional[Tensor],
+                    lse: Tensor, alpha_lr: Tensor, pos_bias: Tensor, scale_embed: Optional[Tensor],
                     score_gain: Optional[Tensor], if_gain: Optional[Tensor], offsets: List[int],
                     need_dse: bool, need_dg: bool,
                     need_da: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """dsqg_bwd_qkv with the injected K/V: (dqkv, dpos_bias, dscale_embed, dscore_gain, dif_gain)."""
-    return _bwd_qkv_impl(qkv, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain,
-                         offsets, need_dse, need_dg, need_da, k_eff, v_eff)
+    return _bwd_qkv_impl(qkv, num_heads, dout, lse, alpha_lr, pos_bias, scale_embed, score_gain,
+                         if_gain, offsets, need_dse, need_dg, need_da, k_eff, v_eff)
 
 
 @dsqg_bwd_qkv_kv.register_fake
-def _(qkv, k_eff, v_eff, num_heads, dout, lse, pos_bias, scale_embed, score_gain, if_gain,
-      offsets, need_dse, need_dg, need_da):
+def _(qkv, k_eff, v_eff, num_heads, dout, lse, alpha_lr, pos_bias, scale_embed, score_gain,
+      if_gain, offsets, need_dse, need_dg, need_da):
     B, N, E3 = qkv.shape
     HD = E3 // (3 * num_heads)
     J = len(offsets)
@@ -401,26 +421,27 @@ def _(qkv, k_eff, v_eff, num_heads, dout, lse, pos_bias, scale_embed, score_gain
 
 def _setup_context_qkv_kv(ctx, inputs, output):
     qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed, score_gain, if_gain, offsets = inputs
-    _, lse, k_eff, v_eff = output
-    ctx.save_for_backward(qkv, k_eff, v_eff, lse, pos_bias, scale_embed, score_gain, if_gain)
+    _, lse, alpha_lr, k_eff, v_eff = output
+    ctx.save_for_backward(qkv, k_eff, v_eff, lse, alpha_lr, pos_bias, scale_embed, score_gain,
+                          if_gain)
     ctx.num_heads = num_heads
     ctx.offsets = list(offsets)
     ctx.delta_dtypes = (k_delta.dtype, v_delta.dtype)
-    ctx.mark_non_differentiable(lse, k_eff, v_eff)
+    ctx.mark_non_differentiable(lse, alpha_lr, k_eff, v_eff)
 
 
-def _backward_qkv_kv(ctx, dout, _dlse, _dk_eff, _dv_eff, direct: bool = False):
-    qkv, k_eff, v_eff, lse, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
+def _backward_qkv_kv(ctx, dout, _dlse, _dalpha, _dk_eff, _dv_eff, direct: bool = False):
+    qkv, k_eff, v_eff, lse, alpha_lr, pos_bias, scale_embed, score_gain, if_gain = ctx.saved_tensors
     need = ctx.needs_input_grad
     need_dse = bool(need[5]) and scale_embed is not None
     need_dg = bool(need[6]) and score_gain is not None
     need_da = bool(need[7]) and if_gain is not None
-    args = (qkv, k_eff, v_eff, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias, scale_embed,
-            score_gain, if_gain, ctx.offsets, need_dse, need_dg, need_da)
+    args = (qkv, k_eff, v_eff, ctx.num_heads, dout.to(qkv.dtype), lse, alpha_lr, pos_bias,
+            scale_embed, score_gain, if_gain, ctx.offsets, need_dse, need_dg, need_da)
     if direct:
         dqkv, dpb, dse, dg, da = _bwd_qkv_impl(
-            qkv, ctx.num_heads, dout.to(qkv.dtype), lse, pos_bias, scale_embed, score_gain,
-            if_gain, ctx.offsets, need_dse, need_dg, need_da, k_eff, v_eff)
+            qkv, ctx.num_heads, dout.to(qkv.dtype), lse, alpha_lr, pos_bias, scale_embed,
+            score_gain, if_gain, ctx.offsets, need_dse, need_dg, need_da, k_eff, v_eff)
     else:
         dqkv, dpb, dse, dg, da = dsqg_bwd_qkv_kv(*args)
     _, dk, dv = split_qkv(dqkv, ctx.num_heads)
@@ -455,13 +476,13 @@ class AttentionFn(torch.autograd.Function):
     def forward(ctx, q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets):
         launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
         launch.run()
-        _setup_context(ctx, (q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets),
-                       (launch.out, launch.lse))
-        return launch.out, launch.lse
+        outs = (launch.out, launch.lse, launch.alpha_lr)
+        _setup_context(ctx, (q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets), outs)
+        return outs
 
     @staticmethod
-    def backward(ctx, dout, dlse):
-        return _backward(ctx, dout, dlse, direct=True)
+    def backward(ctx, dout, dlse, dalpha):
+        return _backward(ctx, dout, dlse, dalpha, direct=True)
 
 
 class AttentionQkvFn(torch.autograd.Function):
@@ -470,13 +491,14 @@ class AttentionQkvFn(torch.autograd.Function):
         q, k, v = split_qkv(qkv, num_heads)
         launch = FwdLaunch(q, k, v, pos_bias, scale_embed, score_gain, if_gain, offsets)
         launch.run()
+        outs = (launch.out, launch.lse, launch.alpha_lr)
         _setup_context_qkv(ctx, (qkv, num_heads, pos_bias, scale_embed, score_gain, if_gain,
-                                 offsets), (launch.out, launch.lse))
-        return launch.out, launch.lse
+                                 offsets), outs)
+        return outs
 
     @staticmethod
-    def backward(ctx, dout, dlse):
-        return _backward_qkv(ctx, dout, dlse, direct=True)
+    def backward(ctx, dout, dlse, dalpha):
+        return _backward_qkv(ctx, dout, dlse, dalpha, direct=True)
 
 
 class AttentionQkvKvFn(torch.autograd.Function):
@@ -487,14 +509,14 @@ class AttentionQkvKvFn(torch.autograd.Function):
         q = split_qkv(qkv, num_heads)[0]
         launch = FwdLaunch(q, k_eff, v_eff, pos_bias, scale_embed, score_gain, if_gain, offsets)
         launch.run()
+        outs = (launch.out, launch.lse, launch.alpha_lr, k_eff, v_eff)
         _setup_context_qkv_kv(ctx, (qkv, k_delta, v_delta, num_heads, pos_bias, scale_embed,
-                                    score_gain, if_gain, offsets),
-                              (launch.out, launch.lse, k_eff, v_eff))
-        return launch.out, launch.lse, k_eff, v_eff
+                                    score_gain, if_gain, offsets), outs)
+        return outs
 
     @staticmethod
-    def backward(ctx, dout, dlse, dk_eff, dv_eff):
-        return _backward_qkv_kv(ctx, dout, dlse, dk_eff, dv_eff, direct=True)
+    def backward(ctx, dout, dlse, dalpha, dk_eff, dv_eff):
+        return _backward_qkv_kv(ctx, dout, dlse, dalpha, dk_eff, dv_eff, direct=True)
 
 
 # ------------------------------------------------------------------------------------------

@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define DSQG_ABI_VERSION 2
+#define DSQG_ABI_VERSION 3
 #define DSQG_MAX_OFFSETS 64
 
 /* Same type as hipStream_t; NULL is the null stream. */
@@ -83,6 +83,10 @@ typedef struct {
 } dsqg_shape;
 
 /* Forward: out [B,H,N,D] (dtype), lse [B,H,N] fp32 contiguous (lse may be NULL).
+ * alpha_lr (bf16 only; NULL = not written, and ignored for fp32): the softmax weights of the
+ * long-range taps, [B,H,NS,N] fp32 contiguous with NS = dsqg_long_range_taps(offsets): saved
+ * for the bf16 backward, which requires them (as the reference saves out and lse,
+ * kernels/dsqg_attention_v3.py:384); dsqg_alpha_lr_elems gives its size.
  * Replaces kernels/dsqg_attention_v3.py:361-387 (_DSQGFnV3.forward). */
 typedef struct {
     dsqg_shape shape;
@@ -95,9 +99,11 @@ typedef struct {
     const float* if_gain;      /* [H]   or NULL */
     void* out;  int64_t out_stride[4];
     float* lse;                /* [B,H,N] or NULL */
+    float* alpha_lr;           /* [B,H,NS,N] or NULL (bf16) */
 } dsqg_fwd_args;
 
-/* Backward.  dout is the gradient of out; lse is the forward's.  dq/dk/dv are written
+/* Backward.  dout is the gradient of out; lse and (bf16, required when the table has taps
+ * beyond its dense window) alpha_lr are the forward's.  dq/dk/dv are written
  * (not accumulated).  dpos_bias [J,H] is required; dscale_embed [J,D], dscore_gain [H,J] and
  * dif_gain [H] are written when non-NULL (they are defined even when the matching input is
  * NULL, i.e. at se = 0, g = 1, a = 1).  The parameter gradients are reduced
@@ -123,6 +129,7 @@ typedef struct {
     float* dif_gain;           /* [H]   or NULL */
     void* workspace;           /* device memory, 256-byte aligned */
     size_t workspace_bytes;
+    const float* alpha_lr;     /* [B,H,NS,N] from dsqg_fwd (bf16); ignored for fp32 */
 } dsqg_bwd_args;
 
 /* Decode step: one new token per sequence.  q, k_new, v_new, out are [B,H,D] contiguous;
@@ -159,6 +166,15 @@ const char* dsqg_status_string(int status);
 int dsqg_supported_head_dims(int32_t* dims, int cap);
 
 int dsqg_fwd(const dsqg_fwd_args* args, dsqg_stream_t stream);
+
+/* Taps beyond the dense window of an offset table (offsets[0..W] = 0..W, W <= 32): the NS of
+ * alpha_lr.  Returns NS >= 0, or a negative DSQG_EINVAL for an invalid table. */
+int dsqg_long_range_taps(const int32_t* offsets, int J);
+
+/* Elements of alpha_lr for a shape (B * H * NS * N; 0 for fp32).  Returns DSQG_OK and writes
+ * *elems, or an argument error.  No counterpart in the reference (which recomputes every score
+ * in its backward). */
+int dsqg_alpha_lr_elems(const dsqg_shape* shape, size_t* elems);
 
 /* Workspace the backward needs for these arguments (shape and which gradients are requested).
  * Returns DSQG_OK and writes *bytes, or an argument error. */

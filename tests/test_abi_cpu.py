@@ -42,9 +42,10 @@ def test_ctypes_layout_matches_c(tmp_path):
     from dwarf_amd import _lib
     probes = {
         "dsqg_shape": (_lib.Shape, ["dtype", "J", "offsets"]),
-        "dsqg_fwd_args": (_lib.FwdArgs, ["q", "k_stride", "pos_bias", "if_gain", "out", "lse"]),
+        "dsqg_fwd_args": (_lib.FwdArgs, ["q", "k_stride", "pos_bias", "if_gain", "out", "lse",
+                                         "alpha_lr"]),
         "dsqg_bwd_args": (_lib.BwdArgs, ["dout", "lse", "dq_stride", "dpos_bias", "dif_gain",
-                                         "workspace", "workspace_bytes"]),
+                                         "workspace", "workspace_bytes", "alpha_lr"]),
         "dsqg_decode_args": (_lib.DecodeArgs, ["S", "q", "pos", "pos_next", "if_gain", "out"]),
         "dsqg_pool_gate_fwd_args": (_lib.PoolFwdArgs, ["out_dtype", "x", "gate_stride", "out",
                                                        "workspace", "workspace_bytes"]),
@@ -134,6 +135,7 @@ def _bwd_args(need_se=True):
         setattr(a, name, fake)
         setattr(a, name + "_stride", f.q_stride)
     a.lse = fake
+    a.alpha_lr = fake
     a.pos_bias = fake
     a.dpos_bias = fake
     a.dscale_embed = fake if need_se else None
@@ -163,6 +165,29 @@ def test_bwd_workspace_query_and_errors(lib):
     assert lib.dsqg_bwd_workspace_size(ctypes.byref(c), None) == _lib.DSQG_EINVAL
     c = _bwd_args(); c.scale_embed = 0x10008             # scale_embed not 16-byte aligned
     assert lib.dsqg_bwd_workspace_size(ctypes.byref(c), ctypes.byref(n0)) == _lib.DSQG_EINVAL
+    c = _bwd_args(); c.alpha_lr = None                   # bf16 needs the forward's alpha_lr
+    assert lib.dsqg_bwd_workspace_size(ctypes.byref(c), ctypes.byref(n0)) == _lib.DSQG_EINVAL
+    assert lib.dsqg_bwd(ctypes.byref(c), None) == _lib.DSQG_EINVAL
+    c = _bwd_args(); c.alpha_lr = 0x10002                # fp32 elements: 4-byte aligned
+    assert lib.dsqg_bwd_workspace_size(ctypes.byref(c), ctypes.byref(n0)) == _lib.DSQG_EINVAL
+
+
+def test_long_range_taps_and_alpha_size(lib):
+    """NS (taps beyond the dense window) of the named tables, and the alpha_lr element count."""
+    from dwarf_amd import _lib
+    from dwarf_amd.offsets import OFFSETS_J46, OFFSETS_J47, OFFSETS_V3
+    for offs, ns in ((OFFSETS_V3, 11), (OFFSETS_J46, 13), (OFFSETS_J47, 14), ((0,), 0),
+                     (tuple(range(48)), 15), ((0, 1, 2, 5, 9, 100), 3)):
+        assert _lib.long_range_taps(offs) == ns, offs
+    arr = (ctypes.c_int32 * 3)(1, 2, 3)
+    assert lib.dsqg_long_range_taps(arr, 3) == -_lib.DSQG_EINVAL   # must start at 0
+    n = ctypes.c_size_t(0)
+    sh = _lib.make_shape(_lib.DSQG_BF16, 2, 3, 100, 64, OFFSETS_V3)
+    assert lib.dsqg_alpha_lr_elems(ctypes.byref(sh), ctypes.byref(n)) == _lib.DSQG_OK
+    assert n.value == 2 * 3 * 11 * 100
+    sh = _lib.make_shape(_lib.DSQG_F32, 2, 3, 100, 64, OFFSETS_V3)
+    assert lib.dsqg_alpha_lr_elems(ctypes.byref(sh), ctypes.byref(n)) == _lib.DSQG_OK
+    assert n.value == 0
 
 
 def test_decode_rejects_bad_arguments(lib):
@@ -279,7 +304,7 @@ def test_bf16_row_span_limit(lib):
         for name in ("q", "k", "v", "dout", "dq", "dk", "dv"):
             setattr(b, name, 0x10000)
             setattr(b, name + "_stride", st)
-        b.lse = b.pos_bias = b.dpos_bias = 0x10000
+        b.lse = b.alpha_lr = b.pos_bias = b.dpos_bias = 0x10000
         n = ctypes.c_size_t(0)
         assert lib.dsqg_bwd_workspace_size(ctypes.byref(b), ctypes.byref(n)) == want, N
     f = _lib.FwdArgs()

@@ -27,26 +27,27 @@ def _t(*shape, dtype=torch.bfloat16, grad=False):
 def test_forward_and_backward_ops(fake):
     q = _t(B, H, N, D)
     pb = _t(J, H, dtype=torch.float32)
-    out, lse = ops.dsqg_fwd(q, q, q, pb, None, None, None, list(OFFSETS_V3))
+    out, lse, alr = ops.dsqg_fwd(q, q, q, pb, None, None, None, list(OFFSETS_V3))
     assert out.shape == (B, H, N, D) and out.dtype == torch.bfloat16
     assert out.stride() == (N * H * D, D, H * D, 1)  # token-major storage
     assert lse.shape == (B, H, N) and lse.dtype == torch.float32
-    grads = ops.dsqg_bwd(q, q, q, q, lse, pb, None, None, None, list(OFFSETS_V3), False, False,
-                         True)
+    assert alr.shape == (B, H, 11, N) and alr.dtype == torch.float32  # 11 long-range taps
+    grads = ops.dsqg_bwd(q, q, q, q, lse, alr, pb, None, None, None, list(OFFSETS_V3), False,
+                         False, True)
     assert [tuple(g.shape) for g in grads] == [(B, H, N, D)] * 3 + [(J, H), (0,), (0,), (H,)]
     qkv = _t(B, N, 3 * H * D)
-    out, lse = ops.dsqg_fwd_qkv(qkv, H, pb, None, None, None, list(OFFSETS_V3))
-    assert out.shape == (B, H, N, D) and lse.shape == (B, H, N)
-    dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv(qkv, H, q, lse, pb, None, None, None,
+    out, lse, alr = ops.dsqg_fwd_qkv(qkv, H, pb, None, None, None, list(OFFSETS_V3))
+    assert out.shape == (B, H, N, D) and lse.shape == (B, H, N) and alr.shape == (B, H, 11, N)
+    dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv(qkv, H, q, lse, alr, pb, None, None, None,
                                               list(OFFSETS_V3), True, True, False)
     assert dqkv.shape == qkv.shape and dse.shape == (J, D) and dg.shape == (H, J)
     # K/V injection: the injected K/V come back for the backward, which returns one d(qkv).
-    out, lse, k_eff, v_eff = ops.dsqg_fwd_qkv_kv(qkv, q, q, H, pb, None, None, None,
-                                                 list(OFFSETS_V3))
-    assert out.shape == (B, H, N, D) and lse.shape == (B, H, N)
+    out, lse, alr, k_eff, v_eff = ops.dsqg_fwd_qkv_kv(qkv, q, q, H, pb, None, None, None,
+                                                      list(OFFSETS_V3))
+    assert out.shape == (B, H, N, D) and lse.shape == (B, H, N) and alr.shape == (B, H, 11, N)
     assert k_eff.shape == (B, H, N, D) and v_eff.shape == (B, H, N, D)
-    dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv_kv(qkv, k_eff, v_eff, H, q, lse, pb, None, None,
-                                                 None, list(OFFSETS_V3), False, False, False)
+    dqkv, dpb, dse, dg, da = ops.dsqg_bwd_qkv_kv(qkv, k_eff, v_eff, H, q, lse, alr, pb, None,
+                                                 None, None, list(OFFSETS_V3), False, False, False)
     assert dqkv.shape == qkv.shape and dpb.shape == (J, H) and dse.numel() == 0
 
 

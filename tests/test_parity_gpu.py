@@ -55,12 +55,12 @@ def oracle_chunked(inp, offsets, dtype, backward=True):
 
 def gpu_run(inp, offsets, dev, backward=True):
     d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
-    out, lse = ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], d.get("scale_embed"),
-                            d.get("score_gain"), d.get("if_gain"), list(offsets))
+    out, lse, alr = ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], d.get("scale_embed"),
+                                 d.get("score_gain"), d.get("if_gain"), list(offsets))
     res = {"out": out, "lse": lse}
     if backward:
         dq, dk, dv, dpb, dse, dg, da = ops.dsqg_bwd(
-            d["q"], d["k"], d["v"], d["dout"], lse, d["pos_bias"], d.get("scale_embed"),
+            d["q"], d["k"], d["v"], d["dout"], lse, alr, d["pos_bias"], d.get("scale_embed"),
             d.get("score_gain"), d.get("if_gain"), list(offsets),
             d.get("scale_embed") is not None, d.get("score_gain") is not None,
             d.get("if_gain") is not None)
@@ -244,7 +244,8 @@ def test_bf16_table_beyond_the_mfma_kernels_is_rejected(gpu_device):
         ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], None, None, None, list(offsets))
     lse = torch.zeros(1, 2, 200, device=gpu_device)
     with pytest.raises(Exception, match="unsupported"):
-        ops.dsqg_bwd(d["q"], d["k"], d["v"], d["dout"], lse, d["pos_bias"], None, None, None,
+        ops.dsqg_bwd(d["q"], d["k"], d["v"], d["dout"], lse, torch.zeros(1, 2, 15, 200, device=gpu_device),
+                     d["pos_bias"], None, None, None,
                      list(offsets), False, False, False)
     f32 = {k: (v.float() if v is not None and v.is_floating_point() else v) for k, v in inp.items()}
     got = gpu_run(f32, offsets, gpu_device)
@@ -309,11 +310,11 @@ def test_strided_views_match_contiguous(gpu_device):
     q, k, v = (t.view(B, N, H, D).permute(0, 2, 1, 3) for t in qkv.split(H * D, dim=-1))
     pb = (torch.randn(44, H, generator=g) * 0.5).to(gpu_device)
     se = (torch.randn(44, D, generator=g) * 0.1).to(gpu_device)
-    o1, l1 = ops.dsqg_fwd(q, k, v, pb, se, None, None, list(OFFSETS_V3))
-    o2, l2 = ops.dsqg_fwd(q.contiguous(), k.contiguous(), v.contiguous(), pb, se, None, None,
+    o1, l1, a1 = ops.dsqg_fwd(q, k, v, pb, se, None, None, list(OFFSETS_V3))
+    o2, l2, a2 = ops.dsqg_fwd(q.contiguous(), k.contiguous(), v.contiguous(), pb, se, None, None,
                           list(OFFSETS_V3))
     assert q.stride(2) == 3 * H * D
-    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2) and torch.equal(a1, a2)
 
 
 def test_misaligned_scale_embed_view_matches_aligned(gpu_device):
@@ -328,11 +329,11 @@ def test_misaligned_scale_embed_view_matches_aligned(gpu_device):
     assert se_view.data_ptr() % 16 == 4 and se_view.is_contiguous()
     runs = []
     for se in (d["scale_embed"], se_view):
-        out, lse = ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], se, d["score_gain"],
-                                d["if_gain"], list(OFFSETS_V3))
-        grads = ops.dsqg_bwd(d["q"], d["k"], d["v"], d["dout"], lse, d["pos_bias"], se,
+        out, lse, alr = ops.dsqg_fwd(d["q"], d["k"], d["v"], d["pos_bias"], se, d["score_gain"],
+                                     d["if_gain"], list(OFFSETS_V3))
+        grads = ops.dsqg_bwd(d["q"], d["k"], d["v"], d["dout"], lse, alr, d["pos_bias"], se,
                              d["score_gain"], d["if_gain"], list(OFFSETS_V3), True, True, True)
-        runs.append((out, lse) + tuple(grads))
+        runs.append((out, lse, alr) + tuple(grads))
     for a, b in zip(*runs):
         assert torch.equal(a, b)
 
@@ -450,7 +451,7 @@ def test_phase_by_phase_backward_equals_full(gpu_device, dtype, D, se):
     for phased in (False, True):
         bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
                            d.get("scale_embed"), d.get("score_gain"), d.get("if_gain"),
-                           list(OFFSETS_V3), se, True, True)
+                           list(OFFSETS_V3), se, True, True, alpha_lr=fl.alpha_lr)
         if phased:
             for phase in ("dq", "dkdv", "params"):
                 bl.run(phase)

@@ -98,8 +98,8 @@ def test_softmax_weights_sum_to_one(gpu_device, dtype, offsets):
     se = torch.randn(J, D) * 0.05
     v = torch.ones(B, H, N, D)
     dev = gpu_device
-    out, lse = ops.dsqg_fwd(q.to(dtype).to(dev), k.to(dtype).to(dev), v.to(dtype).to(dev),
-                            pb.to(dev), se.to(dev), None, None, list(offsets))
+    out, lse, _ = ops.dsqg_fwd(q.to(dtype).to(dev), k.to(dtype).to(dev), v.to(dtype).to(dev),
+                               pb.to(dev), se.to(dev), None, None, list(offsets))
     out = out.float().cpu()
     lo, hi = out.min().item(), out.max().item()
     _say(f"{dtype} J={J}: weight sums in [{lo:.6f}, {hi:.6f}]")
@@ -123,8 +123,8 @@ def test_causality_perturbation(gpu_device, dtype, t):
     d = {n: x.to(dev) for n, x in (("q", q), ("k", k), ("v", v), ("dout", dout), ("pb", pb), ("se", se))}
 
     def run(kk, vv, dd):
-        out, lse = ops.dsqg_fwd(d["q"], kk, vv, d["pb"], d["se"], None, None, list(OFFSETS_V3))
-        dq, dk, dv, *_ = ops.dsqg_bwd(d["q"], kk, vv, dd, lse, d["pb"], d["se"], None, None,
+        out, lse, alr = ops.dsqg_fwd(d["q"], kk, vv, d["pb"], d["se"], None, None, list(OFFSETS_V3))
+        dq, dk, dv, *_ = ops.dsqg_bwd(d["q"], kk, vv, dd, lse, alr, d["pb"], d["se"], None, None,
                                       list(OFFSETS_V3), True, False, False)
         torch.cuda.synchronize(dev)
         return out.cpu(), dq.cpu(), dk.cpu(), dv.cpu()

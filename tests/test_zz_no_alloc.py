@@ -25,7 +25,7 @@ def _big_args():
     for name in ("q", "k", "v", "dout", "dq", "dk", "dv"):
         setattr(a, name, fake)
         setattr(a, name + "_stride", st)
-    a.lse = a.pos_bias = a.dpos_bias = a.dscale_embed = fake
+    a.lse = a.alpha_lr = a.pos_bias = a.dpos_bias = a.dscale_embed = fake
     return a
 
 
@@ -49,7 +49,8 @@ def _case(dev, B, H, N, D, se, gains, seed):
     ig = (torch.rand(H, generator=g) * 0.4 + 0.8).to(dev) if gains else None
     fl = ops.FwdLaunch(q, k, v, pb, sev, sg, ig, list(OFFSETS_V3))
     fl.run()
-    return ops.BwdLaunch(q, k, v, dout, fl.lse, pb, sev, sg, ig, list(OFFSETS_V3), se, gains, gains)
+    return ops.BwdLaunch(q, k, v, dout, fl.lse, pb, sev, sg, ig, list(OFFSETS_V3), se, gains, gains,
+                         alpha_lr=fl.alpha_lr)
 
 
 @pytest.mark.gpu
