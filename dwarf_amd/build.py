@@ -33,6 +33,9 @@ HIPCC_FLAGS = [
     "-fPIC",
     # Packed-FP32 VALU forms are kept out of the generated code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Kernel arguments ahead of any by-value parameter block (the decode step's position and row
+    # pointers) arrive preloaded in scalar registers: no argument round trip before the first load.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wno-unused-command-line-argument",
 ]
 # Set DSQG_RESOURCE_USAGE=1 to print per-kernel VGPR / LDS / spill figures while compiling.

@@ -326,6 +326,7 @@ int dsqg_decode_step(const dsqg_decode_args* a, dsqg_stream_t stream) {
   if (!a->pos || !a->pos_bias) return DSQG_EINVAL;
   if (a->pos_next && a->pos_next == a->pos) return DSQG_EINVAL;
   if (rows > INT_MAX) return DSQG_EINVAL;
+  if (s.H > 4 * 65535) return DSQG_EUNSUPPORTED;  // grid: B sequences x ceil(H / 4) head groups
   p.B = s.B; p.H = s.H; p.S = a->S;
   p.scale = 1.0f / sqrtf((float)s.D);
   p.q = a->q; p.k_new = a->k_new; p.v_new = a->v_new;

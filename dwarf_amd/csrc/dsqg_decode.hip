@@ -6,10 +6,10 @@
 // delta > 0, masked when p - delta < 0.  Because delta < S, no tap slot equals the slot being
 // written, so the write and the reads of one step never touch the same row.
 //
-// One wave64 per (b,h), four per workgroup.  Lanes form R = 64/G groups of G = D/8 lanes; in
-// pass t group r handles tap j = t*R + r, so the J key and value rows are fetched as R
-// coalesced rows at a time, all of them requested before any arithmetic (two dependent memory
-// round trips per step: the position, then the ring rows it selects).  The softmax max/sum
+// One wave64 per (b,h), four heads of one sequence per workgroup.  Lanes form R = 64/G groups of
+// G = D/8 lanes; in pass t group r handles tap j = t*R + r, so the J key and value rows are
+// fetched as R coalesced rows at a time, all of them requested together before any arithmetic
+// (two dependent memory round trips per step: the position, then the ring rows it selects).  The softmax max/sum
 // and the output sum across groups use DPP and v_permlane16/32_swap (no LDS).
 //
 // The reference has no decode kernel (train/train_2048_condU.py:463-487 recomputes the prefix);
@@ -76,48 +76,55 @@ __device__ __forceinline__ void groups_scatter_sum(float (&a)[8]) {
   if constexpr (G == 4) a[0] += __shfl_xor(a[0], 4, 64);
 }
 
+// The position and the row pointers come first, as plain kernel arguments: they are preloaded
+// into scalar registers at wave launch (kernel-argument preloading, gfx950), so the position's
+// load is the first instruction of the wave instead of waiting for a kernel-argument round trip.
 template <typename T, int D, int JMAX, bool HAS_SE>
-__global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(kBlock) void decode_kernel(const long long* __restrict__ pos,
+                                                        long long* __restrict__ pos_next,
+                                                        const T* __restrict__ qp, const T* __restrict__ knp,
+                                                        const T* __restrict__ vnp, T* k_ring, T* v_ring,
+                                                        DecodeParams p) {
   constexpr int G = lanes_per_row(D);  // lanes with 8g >= D (D = 80, 96) hold zeros
   constexpr int R = 64 / G;
   constexpr int P = (JMAX + R - 1) / R;
   constexpr int E = sizeof(T);
 
+  // Sequence b = blockIdx.x, heads 4 * blockIdx.y + wave: no division.  Waves past the last head
+  // (H not a multiple of four) repeat it and store nothing, so that no wave exits early.
+  const int b = blockIdx.x;
   const int lane = threadIdx.x & 63;
-  // The wave index is uniform: readfirstlane keeps (b, h), the row pointers and the ring's buffer
-  // resources in scalar registers (a resource in vector registers costs every load a loop).
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // One round trip for the kernel arguments before the position's: the arguments the prologue
-  // needs pass through one empty asm statement that everything after it depends on, so their
-  // scalar loads go out together and are waited for once (otherwise the compiler waits for B
-  // and H, divides, and only then asks for the pointers).  For the same reason no wave exits
-  // early: waves past the last (b,h) (B * H not a multiple of four) repeat it and store nothing.
-  int nB = p.B, nH = p.H, J = p.taps.J;
-  const long long* posp = p.pos;
-  const void *qp = p.q, *knp = p.k_new, *vnp = p.v_new;
-  const float* pbp = p.pos_bias;
-  asm volatile("" : "+s"(nB), "+s"(nH), "+s"(J) : "s"(posp), "s"(qp), "s"(knp), "s"(vnp), "s"(pbp));
-  const long long nbh = (long long)nB * nH;
-  const long long bh_w = (long long)blockIdx.x * (kBlock / 64) + wave;
-  const bool live = bh_w < nbh;
-  const long long bh = live ? bh_w : nbh - 1;
-  const int b = (int)bh / nH, h = (int)bh - b * nH;  // B * H < 2^31 (checked by the ABI)
   const int r = lane / G, g = lane - r * G;
+  // The two loads the ring rows' addresses need go out first, before any other argument is
+  // read: the position (a vector load of a uniform address, so that waiting for it does not
+  // also wait for the scalar argument loads) and this lane's tap offset of each pass (from the
+  // argument block, whose address every wave has at launch).
+  const long long pos_v = __builtin_nontemporal_load(pos + b + opaque(0));
+  int dlv[P];
+#pragma unroll
+  for (int t = 0; t < P; ++t) {
+    const int j = t * R + r;
+    dlv[t] = p.taps.delta[j < JMAX ? j : 0];  // taps j >= J are masked below
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int H = p.H, J = p.taps.J, S = p.S;
+  const int h0 = (int)blockIdx.y * (kBlock / 64) + wave;
+  const bool live = h0 < H;
+  const int h = live ? h0 : H - 1;
+  const long long bh = (long long)b * H + h;
   const int d0 = g * 8;
   const bool lane_ok = d0 < D;
-  const int S = p.S;
   const float c = p.scale;
-  const long long pos = posp[b];  // waited for at the validity test below
   T* outrow = static_cast<T*>(p.out) + bh * D;
-  const T* qrow = static_cast<const T*>(qp) + bh * D;
-  const T* knew = static_cast<const T*>(knp) + bh * D;
-  const T* vnew = static_cast<const T*>(vnp) + bh * D;
+  const T* qrow = qp + bh * D;
+  const T* knew = knp + bh * D;
+  const T* vnew = vnp + bh * D;
 
-  // Two memory round trips per step.  Everything that does not depend on the position (query,
-  // new key/value row, per-tap bias, gain and scale_embed) is requested before the position is
-  // waited for, and with scale_embed each pass's share of q.se_j is formed meanwhile; the ring
-  // rows of the taps follow the position, all requested before the rest of the arithmetic.
-  // Tap 0 (delta = 0) is the new row, already in registers; so is the row written into the ring.
+  // Everything else that does not depend on the position is requested before it is waited
+  // for: the query, the new key/value row, and per pass this lane's bias, gain and (with
+  // scale_embed) its share of q.se_j.  Tap 0 (delta = 0) is the new row, already in registers;
+  // so is the row written into the ring.
   constexpr int C16 = E == 4 ? 2 : 1;  // 16-byte chunks per lane (8 elements)
   uint4 qraw[C16], knraw[C16], vnraw[C16];
 #pragma unroll
@@ -131,7 +138,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   for (int t = 0; t < P; ++t) {
     const int j = t * R + r;
     const int jj = j < J ? j : 0;
-    pbias[t] = pbp[jj * nH + h];
+    pbias[t] = p.pos_bias[jj * H + h];
     pgain[t] = p.score_gain ? p.score_gain[h * J + jj] : 1.0f;
   }
   float q[8];
@@ -155,8 +162,11 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     }
   }
 
-  if (pos < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
-    if (live && p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos;
+  // The uniform position in scalar registers (the low half zero-extended).
+  const long long pos_b = (long long)(unsigned)__builtin_amdgcn_readfirstlane((int)pos_v) |
+                          ((long long)__builtin_amdgcn_readfirstlane((int)(pos_v >> 32)) << 32);
+  if (pos_b < 0) {  // invalid position: NaN output, ring untouched, pos_next keeps it invalid
+    if (live && pos_next && h == 0 && lane == 0) pos_next[b] = pos_b;
     if (live && lane < G && lane_ok) {
       float o[8];
 #pragma unroll
@@ -165,18 +175,36 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
     }
     return;
   }
-  if (live && p.pos_next && h == 0 && lane == 0) p.pos_next[b] = pos + 1;
+  if (live && pos_next && h == 0 && lane == 0) pos_next[b] = pos_b + 1;
 
-  T* kring = static_cast<T*>(p.k_ring) + bh * (long long)S * D;
-  T* vring = static_cast<T*>(p.v_ring) + bh * (long long)S * D;
-  // Ring reads go through buffer resources over this sequence's ring: a masked tap gets an
-  // offset past the end and reads zeros, so it needs no select in the weighted sum.
+  T* kring = k_ring + bh * (long long)S * D;
+  T* vring = v_ring + bh * (long long)S * D;
+  // Ring reads go through buffer resources over this sequence's ring: a masked tap (and tap 0,
+  // whose row is the new one) gets an offset past the end and reads zeros, so the loads need no
+  // branch and all of them are in flight together.
   const __amdgpu_buffer_rsrc_t rK = __builtin_amdgcn_make_buffer_rsrc(kring, (short)0, S * D * E, 0x00020000);
   const __amdgpu_buffer_rsrc_t rV = __builtin_amdgcn_make_buffer_rsrc(vring, (short)0, S * D * E, 0x00020000);
 
-  // Slot of tap delta: (pos mod S) - delta, wrapped once (0 < delta < S).  The new row goes
-  // into slot pos mod S now: no tap of this step reads that slot.
-  const int base = (pos >> 31) == 0 ? (int)pos % S : (int)(pos % S);  // 32-bit when it fits
+  // Slot of tap delta: (pos mod S) - delta, wrapped once (0 < delta < S).
+  const int base = (pos_b >> 31) == 0 ? (int)pos_b % S : (int)(pos_b % S);  // 32-bit when it fits
+  uint4 kraw[P][C16], vraw[P][C16];
+  bool ok[P];
+#pragma unroll
+  for (int t = 0; t < P; ++t) {
+    const int j = t * R + r;
+    const int dl = dlv[t];
+    ok[t] = j < J && pos_b - dl >= 0;
+    const int sw = base - dl;
+    const unsigned off = ok[t] && dl > 0 && lane_ok ? (unsigned)(((sw < 0 ? sw + S : sw) * D + d0) * E)
+                                                   : 0x80000000u;
+#pragma unroll
+    for (int u = 0; u < C16; ++u) {
+      kraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rK, off + 16 * u, 0, 0));
+      vraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rV, off + 16 * u, 0, 0));
+    }
+  }
+  // The new row goes into slot pos mod S once every ring load is in flight (no tap of this step
+  // reads that slot, and waiting for the new row first would hold the ring loads back).
   if (live && r == 0 && lane_ok) {
 #pragma unroll
     for (int u = 0; u < C16; ++u) {
@@ -184,25 +212,10 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
       st16(vring + base * D + d0 + 4 * u * (E == 4), vnraw[u]);
     }
   }
-  uint4 kraw[P][C16], vraw[P][C16];
-  bool ok[P];
+  // Tap 0 (group 0 of pass 0) takes the new row.
+  if (r == 0) {
 #pragma unroll
-  for (int t = 0; t < P; ++t) {
-    const int j = t * R + r;
-    const int dl = j < J ? p.taps.delta[j] : 0;
-    ok[t] = j < J && pos - dl >= 0;
-    if (dl > 0) {
-      const int sw = base - dl;
-      const unsigned off = ok[t] && lane_ok ? (unsigned)(((sw < 0 ? sw + S : sw) * D + d0) * E) : 0x80000000u;
-#pragma unroll
-      for (int u = 0; u < C16; ++u) {
-        kraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rK, off + 16 * u, 0, 0));
-        vraw[t][u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rV, off + 16 * u, 0, 0));
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < C16; ++u) { kraw[t][u] = knraw[u]; vraw[t][u] = vnraw[u]; }
-    }
+    for (int u = 0; u < C16; ++u) { kraw[0][u] = knraw[u]; vraw[0][u] = vnraw[u]; }
   }
 
   float s[P];
@@ -228,7 +241,7 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
   for (int t = 0; t < P; ++t) mx = fmaxf(mx, s[t]);
   mx = groups_reduce_max<R>(mx);
 
-  // Masked taps have weight exp(-inf) = 0 and zero rows; taps j >= J hold the new row (finite).
+  // Masked taps have weight exp(-inf) = 0 and zero rows.
   float l = 0.f, acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
@@ -268,13 +281,18 @@ __global__ __launch_bounds__(kBlock) void decode_kernel(DecodeParams p) {
 
 template <typename T, int D, int JMAX>
 static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t st) {
-  const long long waves = (long long)p.B * p.H;
-  if (waves == 0) return hipSuccess;
-  const unsigned nb = (unsigned)((waves + (kBlock / 64) - 1) / (kBlock / 64));
+  if ((long long)p.B * p.H == 0) return hipSuccess;
+  const dim3 grid((unsigned)p.B, (unsigned)((p.H + (kBlock / 64) - 1) / (kBlock / 64)));
+  const long long* pos = p.pos;
+  const T* q = static_cast<const T*>(p.q);
+  const T* kn = static_cast<const T*>(p.k_new);
+  const T* vn = static_cast<const T*>(p.v_new);
+  T* kr = static_cast<T*>(p.k_ring);
+  T* vr = static_cast<T*>(p.v_ring);
   if (p.scale_embed)
-    hipLaunchKernelGGL((decode_kernel<T, D, JMAX, true>), dim3(nb), dim3(kBlock), 0, st, p);
+    hipLaunchKernelGGL((decode_kernel<T, D, JMAX, true>), grid, dim3(kBlock), 0, st, pos, p.pos_next, q, kn, vn, kr, vr, p);
   else
-    hipLaunchKernelGGL((decode_kernel<T, D, JMAX, false>), dim3(nb), dim3(kBlock), 0, st, p);
+    hipLaunchKernelGGL((decode_kernel<T, D, JMAX, false>), grid, dim3(kBlock), 0, st, pos, p.pos_next, q, kn, vn, kr, vr, p);
   return hipGetLastError();
 }
 
