@@ -13,14 +13,14 @@
 //  * Long-range taps: query rows m0w + delta + 0..15, loaded whole-row (D/8 lanes per row: the
 //    vector L1 serves that at close to four times the rate of the MFMA operand order).  Their
 //    weights come from launch 1, which has every long-range pair's alpha, u and D' in hand
-//    anyway: per (query, tap) the pair (c g_j dS_j, a alpha_j) as two bf16 in one dword, read
-//    by the lane on key i's diagonal, so this launch computes no long-range score and reads no
-//    long-range lse or D'.  The query / dOut rows are staged in the wave's rows of the (by then
-//    free) window tiles; each tap's diagonal update is one v_mfma_f32_16x16x16_bf16 per 16 head
-//    dims and matrix: a transposed read of the staged rows against a one-hot operand holding the
-//    weight.  (Each of these 11 of the 44 terms of dk and dv carries the 2^-9 relative rounding
-//    of one bf16 weight; the band's 33 keep fp32 weights as hi + lo pairs.)  The LDS fits four
-//    workgroups per CU (three with scale_embed).
+//    anyway: per (query, tap) the pair (c g_j dS_j, a alpha_j) as two bf16 in one dword, so
+//    this launch computes no long-range score and reads no long-range lse or D'.  A tap adds a
+//    scaled query / dOut row to each key's row (no contraction), so it runs on the VALU in the
+//    row layout (v_dot2_f32_bf16 against (w, 0) / (0, w)), after the band's accumulators are
+//    turned into that layout once; no LDS traffic per tap.  (Each of these 11 of the 44 terms
+//    of dk and dv carries the 2^-9 relative rounding of one bf16 weight; the band's 33 keep
+//    fp32 weights as hi + lo pairs.)  The LDS fits four workgroups per CU (three with
+//    scale_embed).
 //  * The dense band's weights enter their MFMAs as bf16 hi + lo pairs (two products each).
 //  * The q.se_j term of the band's scores (scale_embed) is a [query][tap] table per wave computed
 //    on the MFMA (Q SE^T) with se rounded to bf16 (an error of about 2^-9 |c q.se| in the score,
@@ -50,15 +50,20 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
   constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
   constexpr int CPRP = G_::CPRP;          // lanes per row in the row-chunk layout
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
-  constexpr int PF = 2;
+  // Long-range taps in flight: a tap is a few dozen VALU instructions per wave, so the loads
+  // run several taps ahead (as many as the register budget of the occupancy target allows).
+  constexpr int PF = (D == 64 && !HAS_SE) ? 3 : 4;
   // [query][dense tap] table row stride: a 36-word pitch spreads the band's diagonal reads
   // (row 4g + r, tap 4g + r - i) over all 64 banks.
   constexpr int TS = 35;
   constexpr int SEJ = 48;
   constexpr float kLog2e = 1.4426950408889634f;
 
-  __shared__ __align__(16) bf16_t sQ[WIN * RV];
-  __shared__ __align__(16) bf16_t sO[WIN * RV];
+  // Query window, then dOut window (one array: after the band each wave takes a quarter of it
+  // to turn its accumulators into row layout).
+  __shared__ __align__(16) bf16_t sQO[2 * WIN * RV];
+  bf16_t* const sQ = sQO;
+  bf16_t* const sO = sQO + WIN * RV;
   __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
   __shared__ float sT[HAS_SE ? WIN * TS : 1];        // log2e (bias + c q.se), window query x dense tap
   __shared__ float sBias2[kMaxTaps];
@@ -149,18 +154,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
       lq[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rL, (unsigned)(nq * 4), 0, 0)) * kLog2e;
       dq_[4 * qb + r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rP, (unsigned)(nq * 4), 0, 0));
     }
-  // Weights of the long-range taps from launch 1, for the query on this lane's diagonal (query
-  // m + delta; lanes off the diagonal read past the buffer and get zeros), PF taps ahead like the
-  // query rows.  One buffer resource per tap: the [N] dwords of the (b,h) and tap, so a query at
-  // or past N reads as a zero weight.
-  const bool diag = g == (i >> 2);
+  // Weights of the long-range taps from launch 1: each lane reads the dword of the query that its
+  // row-layout rows meet (key row m0w + r, query m0w + r + delta), PF taps ahead like the query
+  // rows.  One buffer resource per tap over the [N] dwords of the (b,h) and tap, so a query at or
+  // past N reads as a zero weight.
   const unsigned* const lwb = reinterpret_cast<const unsigned*>(p.lrw) + (long long)bh * NS * N;
-  unsigned wS[PF];
+  unsigned wS[PF][CHW];
   auto load_w = [&](int t) {
     const __amdgpu_buffer_rsrc_t rW =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(lwb + (long long)t * N), (short)0, N * 4, 0x00020000);
-    const unsigned off = diag ? (unsigned)(m + dl_s[t]) * 4u : 0x80000000u;
-    wS[t % PF] = __builtin_amdgcn_raw_buffer_load_b32(rW, off, 0, 0);
+#pragma unroll
+    for (int u = 0; u < CHW; ++u)
+      wS[t % PF][u] = __builtin_amdgcn_raw_buffer_load_b32(rW, (unsigned)(m0w + rc_row<D>(l, u) + dl_s[t]) * 4u, 0, 0);
   };
 
   if (tid < J) {
@@ -251,81 +256,94 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     }
   }
 
-  // ---- Long-range taps: queries m0w + delta + 0..15, diagonal of one tile each. ----
+  // ---- Long-range taps: queries m0w + delta + 0..15, one per key row. ----
+  // Each tap adds a scaled query / dOut row to each key's dk / dv row (dk_m += c g_j dS q_n,
+  // dv_m += a alpha_j dOut_n with n = m + delta_j): no contraction, so it runs on the VALU in
+  // the row layout the gathered rows arrive in (D/8 lanes per row, 8 elements per lane), as
+  // v_dot2_f32_bf16 against (w, 0) and (0, w) (exact products of the bf16 row and bf16 weight,
+  // fp32 sums), with no LDS staging and no wait per tap.  The band's MFMA accumulators are first
+  // turned into that layout through the wave's share of the (now free) window tiles.
   // Their first loads are issued only now: during the band the registers hold the band's
-  // operands, and four workgroups per CU cover the wait.
+  // operands, and four workgroups per CU cover the wait.  Scheduling barriers keep every tap's
+  // loads where they stand (the scheduler otherwise hoists later taps' loads over the
+  // conversion and the earlier taps' sums, and their registers spill).
+  uint4 qS[PF][CHW], oS[PF][CHW];
+  auto load_tap = [&](int t) {
+    load_w(t);
+    const int n0 = m0w + dl_s[t];
+#pragma unroll
+    for (int u = 0; u < CHW; ++u) {
+      qS[t % PF][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
+      oS[t % PF][u] = bload16(rO, n0 * dosn + olaneR[u]);
+    }
+  };
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < PF; ++t)
-    if (NSC > 0 ? t < NSC : t < NS) load_w(t);
-  // Long-range query / dOut rows m0w + delta + 0..15, whole rows per D/8 lanes, PF taps ahead.
-  uint4 qS[PF][CHW], oS[PF][CHW];
-#pragma unroll
-  for (int t = 0; t < PF; ++t) {
-    if (t < NS) {
-      const int n0 = m0w + dl_s[t];
-#pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        qS[t][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
-        oS[t][u] = bload16(rO, n0 * dosn + olaneR[u]);
-      }
-    }
-  }
-  // The wave's long-range query / dOut rows are staged in the window tiles (rows 16w..16w+15),
-  // free once every wave's band is done.
-  bf16_t* qsw = sQ + w * 16 * RV;
-  bf16_t* osw = sO + w * 16 * RV;
-  const bf16_t* qtr = qsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
-  const bf16_t* otr = osw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+    if (t < NS) load_tap(t);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // MFMA layout (lane (i, g): key i, d = 16 db + 4 g + 0..3) -> row layout (lane: key row
+  // rc_row, d = 8 rc_chunk + 0..7), fp32, one matrix at a time through the wave's quarter of
+  // the window tiles (row stride DP + 4 floats: conflict-free 16-byte writes and reads).
+  constexpr int CS = G_::DP + 4;
+  static_assert(16 * CS * 4 <= 2 * WIN * RV * 2 / 4, "row-layout staging fits a quarter of the window tiles");
+  float* const cvt = reinterpret_cast<float*>(sQO) + w * (2 * WIN * RV / 2 / 4);
+  float kacc[CHW][8], vacc[CHW][8];
   __syncthreads();  // every wave's band reads of sQ / sO are done
+  auto to_rows = [&](const f32x4_t (&acc)[DB], float (&dst)[CHW][8]) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      *reinterpret_cast<float4*>(cvt + i * CS + 16 * db + 4 * g) = make_float4(acc[db][0], acc[db][1], acc[db][2], acc[db][3]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the quads are written
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < CHW; ++u) {
+      const bool ok = rc_valid<D>(l, u);
+      const float* src = cvt + rc_row<D>(l, u) * CS + 8 * (ok ? rc_chunk<D>(l, u) : 0);
+      const float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+      dst[u][0] = ok ? lo.x : 0.f; dst[u][1] = ok ? lo.y : 0.f; dst[u][2] = ok ? lo.z : 0.f; dst[u][3] = ok ? lo.w : 0.f;
+      dst[u][4] = ok ? hi.x : 0.f; dst[u][5] = ok ? hi.y : 0.f; dst[u][6] = ok ? hi.z : 0.f; dst[u][7] = ok ? hi.w : 0.f;
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are read before the next matrix
+    __builtin_amdgcn_wave_barrier();
+  };
+  to_rows(dK, kacc);
+  to_rows(dV, vacc);
+  __builtin_amdgcn_sched_barrier(0);
+
 #pragma unroll
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
-      // This tap's weights (taken before the ring slot is refilled for tap t + PF).
-      const unsigned wt = wS[t % PF];
+      const int slot = t % PF;
 #pragma unroll
       for (int u = 0; u < CHW; ++u) {
-        if (rc_valid<D>(l, u)) {
-          st16(qsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qS[t % PF][u]);
-          st16(osw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, oS[t % PF][u]);
+        // This row's weights: bf16 dk weight in the low half, bf16 dv weight in the high half.
+        const unsigned wt = wS[slot][u];
+        const unsigned wk0 = wt & 0xffffu, wk1 = wt << 16, wv0 = wt >> 16, wv1 = wt & 0xffff0000u;
+        const uint4 qv = qS[slot][u], ov = oS[slot][u];
+        const unsigned qw[4] = {qv.x, qv.y, qv.z, qv.w}, ow[4] = {ov.x, ov.y, ov.z, ov.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          kacc[u][2 * e] = dot2_bf16_bits(qw[e], wk0, kacc[u][2 * e]);
+          kacc[u][2 * e + 1] = dot2_bf16_bits(qw[e], wk1, kacc[u][2 * e + 1]);
+          vacc[u][2 * e] = dot2_bf16_bits(ow[e], wv0, vacc[u][2 * e]);
+          vacc[u][2 * e + 1] = dot2_bf16_bits(ow[e], wv1, vacc[u][2 * e + 1]);
         }
       }
-      if (t + PF < NS) {
-        load_w(t + PF);
-        const int n0 = m0w + dl_s[t + PF];
+      // The tap's sums are due here (the empty asm pins them: the sums are pure arithmetic, which
+      // instruction selection otherwise sinks past every later tap's loads to the stores).
 #pragma unroll
-        for (int u = 0; u < CHW; ++u) {
-          qS[t % PF][u] = bload16(rQ, n0 * qsn + qlaneR[u]);
-          oS[t % PF][u] = bload16(rO, n0 * dosn + olaneR[u]);
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the staged rows are written
-      __builtin_amdgcn_wave_barrier();
-      // One-hot weights: key i's in the diagonal lane (i, i / 4), element i % 4 (the other
-      // lanes hold zeros), the dk weight from the low half of the dword, the dv weight from the
-      // high half.
-      const s16x4_t bk = onehot_bf16_bits(wt & 0xffffu, i & 3);
-      const s16x4_t bv = onehot_bf16_bits(wt >> 16, i & 3);
+      for (int u = 0; u < CHW; ++u)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const s16x4_t qt = lds_read_tr16(qtr + 16 * db), ot = lds_read_tr16(otr + 16 * db);
-        dK[db] = mfma_16x16x16(qt, bk, dK[db]);
-        dV[db] = mfma_16x16x16(ot, bv, dV[db]);
-      }
+        for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(kacc[u][e]), "+v"(vacc[u][e]));
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + PF < NS) load_tap(t + PF);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // dk, dv (MFMA layout: lane (i, g) holds key i, d = 16 db + 4 g + 0..3) leave as whole rows
-  // through the wave's staging rows of the window tiles (free after the last tap), then 16-byte
-  // row pieces per lane.
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last tap's transposed reads are done
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int db = 0; db < DB; ++db) {
-    *reinterpret_cast<uint2*>(qsw + i * RV + 16 * db + 4 * g) = pack_bf16x4_u2(dK[db][0], dK[db][1], dK[db][2], dK[db][3]);
-    *reinterpret_cast<uint2*>(osw + i * RV + 16 * db + 4 * g) = pack_bf16x4_u2(dV[db][0], dV[db][1], dV[db][2], dV[db][3]);
-  }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
-  __builtin_amdgcn_wave_barrier();
+  // dk, dv leave as whole rows straight from the row layout: 16-byte pieces per lane.
   {
     bf16_t* dkb = static_cast<bf16_t*>(p.dk) + b * p.dks.b + h * p.dks.h;
     bf16_t* dvb = static_cast<bf16_t*>(p.dv) + b * p.dvs.b + h * p.dvs.h;
@@ -333,8 +351,13 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
     for (int u = 0; u < CHW; ++u) {
       const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
       if (m0w + rr < N && cc < CPR) {
-        st16(dkb + (m0w + rr) * p.dks.n + 8 * cc, *reinterpret_cast<const uint4*>(qsw + rr * RV + 8 * cc));
-        st16(dvb + (m0w + rr) * p.dvs.n + 8 * cc, *reinterpret_cast<const uint4*>(osw + rr * RV + 8 * cc));
+        uint4 kp, vp;
+        kp.x = cvt_pk_bf16(kacc[u][0], kacc[u][1]); kp.y = cvt_pk_bf16(kacc[u][2], kacc[u][3]);
+        kp.z = cvt_pk_bf16(kacc[u][4], kacc[u][5]); kp.w = cvt_pk_bf16(kacc[u][6], kacc[u][7]);
+        vp.x = cvt_pk_bf16(vacc[u][0], vacc[u][1]); vp.y = cvt_pk_bf16(vacc[u][2], vacc[u][3]);
+        vp.z = cvt_pk_bf16(vacc[u][4], vacc[u][5]); vp.w = cvt_pk_bf16(vacc[u][6], vacc[u][7]);
+        st16(dkb + (m0w + rr) * p.dks.n + 8 * cc, kp);
+        st16(dvb + (m0w + rr) * p.dvs.n + 8 * cc, vp);
       }
     }
   }

@@ -64,6 +64,13 @@ __device__ __forceinline__ float dot8_bf16(uint4 a, uint4 b, float acc) {
   return acc;
 }
 
+// acc + a.x b.x + a.y b.y for two bf16 pairs given as dword bit patterns (v_dot2_f32_bf16:
+// exact products, fp32 sum).  With b = (w, 0) or (0, w) it adds w times one element of a.
+__device__ __forceinline__ float dot2_bf16_bits(unsigned a, unsigned b, float acc) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
 // Head-dim geometry of the bf16 MFMA kernels; D is a multiple of 16 in [32, 128].
 //  * The MFMA K-steps cover DP = D rounded up to 32.  For D = 80 the 16 extra columns are zero
 //    in every operand (loaded as zeros, staged as zeros).
