@@ -11,12 +11,12 @@
 //     over the row's lanes); each row's u goes to the wave's [query][tap] table in LDS without a
 //     wait per tap.  Then D' = sum_j alpha_j u_j (= dOut . o, pre-gain o) is exact (fp32 weights).
 //  3. With D' known, dS_j = a alpha_j (u_j - D') and dq = c sum_j dS_j (g_j k_j + se_j):
-//     the band's part as MFMAs K^T (c g dS)^T with K^T from LDS (ds_read_tr16_b64), then
-//     long-range pass 2, K rows only: each tap's 16 key rows (gathered whole-row) are staged in
-//     the wave's LDS block and read back transposed against a one-hot operand held by the
-//     query's diagonal lane.  Every weight enters its MFMA as a bf16 hi + lo pair, so the
-//     products keep fp32 weights, as the reference's fp32 sums do (kernels/dsqg_attention_v3.py:
-//     257-271).
+//     the band's part as MFMAs K^T (c g dS)^T with K^T from LDS (ds_read_tr16_b64), whose weights
+//     enter as bf16 hi + lo pairs, so the products keep fp32 weights, as the reference's fp32
+//     sums do (kernels/dsqg_attention_v3.py:257-271).  The accumulators then turn into the row
+//     layout once, and long-range pass 2, K rows only, adds each tap's scaled key row to each
+//     query's row (no contraction) with fp32 FMAs on the VALU: exact bf16 keys, fp32 weights,
+//     no LDS staging per tap.
 //  4. dS fills the per-wave [query][tap] table, from which the workgroup sums dbias (and dg, da)
 //     in a fixed order and dse = c sum_q dS q runs on the MFMA (Q^T dS over the tile's 64 queries,
 //     its [D x J] output tiles split over the four waves).  Every long-range pair's dk/dv weights,
@@ -27,7 +27,7 @@
 // and in dse is split the same way, so these products carry se and dS at fp32 precision.
 // The long-range taps' scores are not recomputed: their alpha comes from the forward.  With the
 // score gain's gradient requested, c q.k of every pair is also needed: the band's from S, the
-// long-range taps' from a dot product with the staged key rows in pass 2.
+// long-range taps' from a dot product with the gathered key rows in pass 2.
 //
 // Follows _compute_D_v3 + _bwd_dq_v3 (kernels/dsqg_attention_v3.py:170-275), except that D' is
 // computed from the fp32 weights and the parameter gradients avoid atomics.
@@ -73,8 +73,8 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   __shared__ __align__(16) bf16_t sK[WIN * RV];        // dense-window K rows
   __shared__ __align__(16) bf16_t sV[WIN * RV];        // dense-window V rows
   // Wave-private staging block: with scale_embed first the dense-tap table
-  // T[i][j] = log2e (bias_j + c q_i.se_j), then the long-range K rows, then the wave's Q rows
-  // (read by every wave for dse).
+  // T[i][j] = log2e (bias_j + c q_i.se_j); then the two rounds that turn dq into row layout;
+  // then, with scale_embed, the wave's Q rows (read by every wave for dse).
   __shared__ __align__(16) bf16_t sKs[4][HAS_SE ? KSB : 16 * RV];
   // scale_embed rows as two bf16 planes, hi = bf16(se) and lo = bf16(se - hi): q.se and
   // SE^T dS then carry se to about 2^-17 relative, as the fp32 se of the reference.
@@ -370,49 +370,132 @@ void bwd_dq_mfma_kernel(BwdParams p) {
     }
   }
 
-  // Long-range pass 2 (diagonal of one 16x16 tile per tap): the tap's key rows are staged in
-  // the wave's block (natural row order) for the transposing reads.
-  unsigned* const lw = reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N + n;
-  const bf16_t* ksr = sKsw + (4 * g + (i >> 2)) * RV + 4 * (i & 3);
+  // dS of every long-range pair, on the query's diagonal lane: into the table (for the SE term,
+  // the parameter sums and pass 2) and, with a alpha_j, to launch 2's weights.
+  {
+    unsigned* const lw = reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N + n;
 #pragma unroll
-  for (int t = 0; t < NSM; ++t) {
-    if (NSC > 0 || t < NS) {
-      const int j = W + 1 + t;
-      const int slot = (NS + t) % PF;
-#pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, rS[slot][u]);
-        if constexpr (DG) {
-          const float qk = group_sum<CPRP>(dot8_bf16(qR[u], rS[slot][u], 0.f));
-          if (rc_chunk<D>(l, u) == 0) sRAWw[rc_row<D>(l, u) * TS + j] = c * qk;
+    for (int t = 0; t < NSM; ++t) {
+      if (NSC > 0 || t < NS) {
+        const int j = W + 1 + t;
+        const float ds = a * als[t] * (uus[t] - Dp);  // zero for masked taps and rows past N
+        if (diag) {
+          sDSw[i * TS + j] = ds;
+          if (row_ok) lw[(long long)t * N] = cvt_pk_bf16(c * sGain[j] * ds, a * als[t]);
         }
       }
-      if (NS + t + PF < 2 * NS) load_rows(NS + t + PF);
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
-      __builtin_amdgcn_wave_barrier();
-      const float ds = a * als[t] * (uus[t] - Dp);  // zero off the diagonal and for masked taps
-      const float wq = c * sGain[j] * ds;
-      if (diag) {
-        sDSw[i * TS + j] = ds;
-        if (row_ok) lw[(long long)t * N] = cvt_pk_bf16(wq, a * als[t]);
-      }
-      s16x4_t bw, bwl;
-      split_onehot_bf16x4(wq, i & 3, bw, bwl);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's table is complete
+  __builtin_amdgcn_wave_barrier();
+
+  if constexpr (HAS_SE) {
+    // SE^T (c dS)^T from this wave's own table rows: dq's scale_embed term.
+#pragma unroll
+    for (int jb = 0; jb < 3; ++jb) {
+      const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
+      s16x4_t bs, bsl;
+      split_bf16x4(c * d4.x, c * d4.y, c * d4.z, c * d4.w, bs, bsl);
+      const int so = (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const s16x4_t at = lds_read_tr16(ksr + 16 * db);
-        X[db] = mfma_16x16x16(at, bw, X[db]);
-        X[db] = mfma_16x16x16(at, bwl, X[db]);
+        const s16x4_t sh = lds_read_tr16(sSE + so + 16 * db);
+        X[db] = mfma_16x16x16(sh, bs, X[db]);
+        X[db] = mfma_16x16x16(sh, bsl, X[db]);
+        X[db] = mfma_16x16x16(lds_read_tr16(sSElo + so + 16 * db), bs, X[db]);
       }
-      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // X (MFMA layout: lane (i, g) holds query i, d = 16 db + 4 g + 0..3) -> row layout (lane: row
+  // rc_row, d = 8 rc_chunk + 0..7), fp32, in two rounds of DP/2 columns through the wave's staging
+  // block (row stride DP/2 + 4 floats: conflict-free 16-byte writes and reads; a round fills the
+  // block exactly).
+  float xacc[CHW][8];
+  {
+    constexpr int HC = G_::DP / 2;  // columns per round
+    constexpr int CS = HC + 4;
+    constexpr int CPH = HC / 8;     // row chunks per round
+    static_assert(16 * CS * 4 <= (HAS_SE ? KSB : 16 * RV) * 2, "a round fits the staging block");
+    float* const cvt = reinterpret_cast<float*>(sKsw);
+#pragma unroll
+    for (int u = 0; u < CHW; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xacc[u][e] = 0.f;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int db = hf * HC / 16; db < (hf + 1) * HC / 16 && db < DB; ++db)
+        *reinterpret_cast<float4*>(cvt + i * CS + 16 * db - hf * HC + 4 * g) =
+            make_float4(X[db][0], X[db][1], X[db][2], X[db][3]);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the quads are written
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) {
+        const int cc = rc_chunk<D>(l, u);
+        if (cc < CPR && cc / CPH == hf) {
+          const float* src = cvt + rc_row<D>(l, u) * CS + 8 * (cc - hf * CPH);
+          const float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+          xacc[u][0] = lo.x; xacc[u][1] = lo.y; xacc[u][2] = lo.z; xacc[u][3] = lo.w;
+          xacc[u][4] = hi.x; xacc[u][5] = hi.y; xacc[u][6] = hi.z; xacc[u][7] = hi.w;
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are read before the next round
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+
+  // ---- Long-range pass 2, K rows: dq_n += c g_j dS_j(n) k_j, one scaled key row per query row. ----
+  // No contraction: fp32 FMAs in the row layout the gathered rows arrive in, against the exact
+  // fp32 weight (read from the table by each row's lanes, one tap ahead), with no LDS staging and
+  // no wait per tap.
+  {
+    float wnx[CHW];
+    auto read_w = [&](int t) {
+      const float cg = c * sGain[W + 1 + t];
+#pragma unroll
+      for (int u = 0; u < CHW; ++u) wnx[u] = cg * sDSw[rc_row<D>(l, u) * TS + W + 1 + t];
+    };
+    read_w(0);
+#pragma unroll
+    for (int t = 0; t < NSM; ++t) {
+      if (NSC > 0 || t < NS) {
+        const int slot = (NS + t) % PF;
+        float wc[CHW];
+#pragma unroll
+        for (int u = 0; u < CHW; ++u) wc[u] = wnx[u];
+        if (t + 1 < NS) read_w(t + 1);
+#pragma unroll
+        for (int u = 0; u < CHW; ++u) {
+          const uint4 kv = rS[slot][u];
+          const unsigned kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            xacc[u][2 * e] = fmaf(wc[u], __builtin_bit_cast(float, kw[e] << 16), xacc[u][2 * e]);
+            xacc[u][2 * e + 1] = fmaf(wc[u], __builtin_bit_cast(float, kw[e] & 0xffff0000u), xacc[u][2 * e + 1]);
+          }
+          if constexpr (DG) {
+            const float qk = group_sum<CPRP>(dot8_bf16(qR[u], kv, 0.f));
+            if (rc_chunk<D>(l, u) == 0) sRAWw[rc_row<D>(l, u) * TS + W + 1 + t] = c * qk;
+          }
+        }
+        // The tap's sums are due here (the empty asm pins them: pure arithmetic is otherwise sunk
+        // past every later tap's loads), and each tap's loads stay in its own iteration.
+#pragma unroll
+        for (int u = 0; u < CHW; ++u)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(xacc[u][e]));
+        __builtin_amdgcn_sched_barrier(0);
+        if (NS + t + PF < 2 * NS) load_rows(NS + t + PF);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
   if constexpr (HAS_SE) {
-    // The wave's Q rows (natural order) replace its K rows, for dse once every table is done.
+    // The wave's Q rows (natural order) replace the conversion rounds in its staging block, for
+    // dse once every table is done.
     if (se_grad) {
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last tap's transposed reads are done
-      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int u = 0; u < CHW; ++u)
         if (rc_valid<D>(l, u)) st16(sKsw + rc_row<D>(l, u) * RV + rc_chunk<D>(l, u) * 8, qR[u]);
@@ -442,22 +525,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
 #pragma unroll
   for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
   if constexpr (HAS_SE) {
-    // SE^T (c dS)^T from this wave's own table rows: dq's scale_embed term.
-#pragma unroll
-    for (int jb = 0; jb < 3; ++jb) {
-      const float4 d4 = *reinterpret_cast<const float4*>(sDSw + i * TS + 16 * jb + 4 * g);
-      s16x4_t bs, bsl;
-      split_bf16x4(c * d4.x, c * d4.y, c * d4.z, c * d4.w, bs, bsl);
-      const int so = (16 * jb + 4 * g + (i >> 2)) * RV + 4 * (i & 3);
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const s16x4_t sh = lds_read_tr16(sSE + so + 16 * db);
-        X[db] = mfma_16x16x16(sh, bs, X[db]);
-        X[db] = mfma_16x16x16(sh, bsl, X[db]);
-        X[db] = mfma_16x16x16(lds_read_tr16(sSElo + so + 16 * db), bs, X[db]);
-      }
-    }
-    __syncthreads();  // all waves' tables and Q rows are complete, all band reads of sK done
+    __syncthreads();  // all waves' tables and Q rows are complete
     // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j) over the tile's 64
     // queries; wave w owns the output tiles w, w+4, ... of the 3 x DB grid.
     if (se_grad) {
@@ -481,34 +549,16 @@ void bwd_dq_mfma_kernel(BwdParams p) {
     }
   }
 
-  // dq (MFMA layout: lane (i, g) holds query i, d = 16 db + 4 g + 0..3) leaves as whole rows
-  // through a wave-private LDS block: the K staging block, or with scale_embed (whose staging
-  // block holds the Q rows for dse) the wave's rows of the K window, free after the barrier
-  // above.  Without such a block (scale_embed at D = 32, whose tables stay outside the V window)
-  // the quads are stored directly.
-  if constexpr (!HAS_SE || TBL_IN_V) {
-    if constexpr (!HAS_SE) {
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the last tap's transposed reads are done
-      __builtin_amdgcn_wave_barrier();
+  // dq leaves as whole rows straight from the row layout: 16-byte pieces per lane.
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+    if (n0w + rr < N && cc < CPR) {
+      uint4 o;
+      o.x = cvt_pk_bf16(xacc[u][0], xacc[u][1]); o.y = cvt_pk_bf16(xacc[u][2], xacc[u][3]);
+      o.z = cvt_pk_bf16(xacc[u][4], xacc[u][5]); o.w = cvt_pk_bf16(xacc[u][6], xacc[u][7]);
+      st16(dqb + (n0w + rr) * p.dqs.n + 8 * cc, o);
     }
-    bf16_t* const stg = HAS_SE ? sK + 16 * w * RV : sKsw;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-      *reinterpret_cast<uint2*>(stg + i * RV + 16 * db + 4 * g) =
-          pack_bf16x4_u2(X[db][0], X[db][1], X[db][2], X[db][3]);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the rows are staged
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int u = 0; u < CHW; ++u) {
-      const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
-      if (n0w + rr < N && cc < CPR)
-        st16(dqb + (n0w + rr) * p.dqs.n + 8 * cc, *reinterpret_cast<const uint4*>(stg + rr * RV + 8 * cc));
-    }
-  } else if (row_ok) {
-    bf16_t* o = dqb + n * p.dqs.n + 4 * g;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-      *reinterpret_cast<uint2*>(o + 16 * db) = pack_bf16x4_u2(X[db][0], X[db][1], X[db][2], X[db][3]);
   }
   if (row_ok && g == 0) p.dpre[rowbase + n] = Dp;
 
