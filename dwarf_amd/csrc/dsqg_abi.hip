@@ -112,7 +112,7 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   p->B = s.B; p->H = s.H; p->N = s.N;
   p->qs = to_strides(a->q_stride); p->ks = to_strides(a->k_stride);
   p->vs = to_strides(a->v_stride); p->dos = to_strides(a->dout_stride);
-  bwd_plan(*p, s.D, s.dtype);
+  bwd_plan(*p, s.D, s.dtype, a->scale_embed != nullptr || a->dscale_embed != nullptr);
   if (s.dtype == DSQG_BF16 && !bwd_mfma_supported(*p, s.D, s.dtype)) return DSQG_EUNSUPPORTED;
   if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;
   if ((long long)s.B * s.H * p->n_tiles_kv > INT_MAX / 2) return DSQG_EINVAL;

@@ -45,18 +45,19 @@ bool bwd_mfma_supported(const BwdParams& p, int D, int dtype) {
          rmin >= D && span < (1LL << 31);
 }
 
-void bwd_plan(BwdParams& p, int D, int dtype) {
+void bwd_plan(BwdParams& p, int D, int dtype, bool se) {
   const bool mfma = bwd_mfma_supported(p, D, dtype);
   const int QPB = mfma ? 64 : kBlock / lanes_per_row(D);  // dq rows per tile
   const int KPB = mfma ? 64 : kBlock / lanes_per_row(D);  // dk/dv rows per workgroup
   p.n_tiles = (p.N + QPB - 1) / QPB;
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
-  // One tile per workgroup: the partial rows (J floats, and J x D for dscale_embed) are small next
-  // to a tile's loads, and the MFMA kernels' single-tile form keeps no per-lane addresses across
-  // tiles (a tile loop costs them a third of their registers; with scale_embed two tiles per
-  // workgroup spilled 116 registers).
-  p.tiles_per_block = 1;
-  p.n_chunks = p.n_tiles;
+  // One tile per workgroup: the partial rows (J floats) are small next to a tile's loads, and the
+  // single-tile form keeps no per-lane addresses across tiles.  The bf16 dq with scale_embed
+  // takes four consecutive tiles per workgroup instead: its [J x D] fp32 dse partial is as large
+  // as a tile's dS, so one per tile costs as many bytes again as the tile's dq (written, then
+  // read back by the reduction); four tiles per partial cut those bytes to a quarter.
+  p.tiles_per_block = (mfma && se) ? 4 : 1;
+  p.n_chunks = (p.n_tiles + p.tiles_per_block - 1) / p.tiles_per_block;
 }
 
 hipError_t launch_bwd_reduce_se_stage(const ReduceParams& r, hipStream_t st) {

@@ -37,7 +37,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 4))) void bwd_dkdv_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : 4)) void bwd_dkdv_mfma_kernel(BwdParams p) {
   using G_ = Geo<D>;
   constexpr int KT = 64;                  // key rows per workgroup
   constexpr int KS = G_::KS;
@@ -53,22 +53,27 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
   // Long-range taps in flight: a tap is a few dozen VALU instructions per wave, so the loads
   // run several taps ahead (as many as the register budget of the occupancy target allows).
   constexpr int PF = (D == 64 && !HAS_SE) ? 3 : 4;
-  // [query][dense tap] table row stride: a 36-word pitch spreads the band's diagonal reads
-  // (row 4g + r, tap 4g + r - i) over all 64 banks.
-  constexpr int TS = 35;
+  // [query][dense tap] table, row stride 33 (the dense taps): the band's diagonal reads (row
+  // 4g + r, tap 4g + r - i) meet at most two to a bank, as with any stride of 33..35, and the
+  // table stays small enough for four workgroups per CU.
+  constexpr int TS = 33;
   constexpr int SEJ = 48;
   constexpr float kLog2e = 1.4426950408889634f;
 
   // Query window, then dOut window (one array: after the band each wave takes a quarter of it
-  // to turn its accumulators into row layout).
+  // to turn its accumulators into row layout).  With scale_embed the se rows sit in the dOut
+  // window until the T table is built, and the dOut rows are stored after it: the workgroup's LDS
+  // then fits four workgroups per CU (40 KB each at D = 64).
   __shared__ __align__(16) bf16_t sQO[2 * WIN * RV];
   bf16_t* const sQ = sQO;
   bf16_t* const sO = sQO + WIN * RV;
-  __shared__ __align__(16) bf16_t sSE[HAS_SE ? SEJ * RV : 8];
+  static_assert(SEJ <= WIN, "the se rows fit the dOut window");
+  bf16_t* const sSE = sO;
   __shared__ float sT[HAS_SE ? WIN * TS : 1];        // log2e (bias + c q.se), window query x dense tap
+  auto t_at = [&](int row, int j) { return row * TS + j; };
   __shared__ float sBias2[kMaxTaps];
   __shared__ float sGain2[kMaxTaps];                 // gain * c * log2e
-  __shared__ float sGainC[kMaxTaps];                 // gain * c
+  __shared__ float sGainC[HAS_SE ? 1 : kMaxTaps];    // gain * c (with scale_embed: sGain2 ln 2)
 
   const int tid = threadIdx.x;
   // Workgroups past the dk/dv tiles run the parameter reduction (partials from launch 1).
@@ -171,17 +176,18 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
   if (tid < J) {
     sBias2[tid] = bias_ld * kLog2e;
     sGain2[tid] = gain_ld * c2;
-    sGainC[tid] = gain_ld * c;
+    if constexpr (!HAS_SE) sGainC[tid] = gain_ld * c;
   }
   if constexpr (HAS_SE) seR.template store<RV>(sSE, nullptr, tid);
+  auto store_window = [&](bf16_t* dst, const uint4 (&src)[CWIN]) {
 #pragma unroll
-  for (int u = 0; u < CWIN; ++u) {
-    const int ci = tid + u * kBlock;
-    if (ci < WIN * CPS) {
-      st16(sQ + (ci / CPS) * RV + (ci % CPS) * 8, wq[u]);
-      st16(sO + (ci / CPS) * RV + (ci % CPS) * 8, wo[u]);
+    for (int u = 0; u < CWIN; ++u) {
+      const int ci = tid + u * kBlock;
+      if (ci < WIN * CPS) st16(dst + (ci / CPS) * RV + (ci % CPS) * 8, src[u]);
     }
-  }
+  };
+  store_window(sQ, wq);
+  if constexpr (!HAS_SE) store_window(sO, wo);
   __syncthreads();
 
   if constexpr (HAS_SE) {
@@ -200,10 +206,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
         const int j = 16 * jb + i;  // column = tap, rows = queries 4g + r
         if (j <= W) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sT[(16 * blk + 4 * g + r) * TS + j] = fmaf(c2, acc[r], sBias2[j]);
+          for (int r = 0; r < 4; ++r) sT[t_at(16 * blk + 4 * g + r, j)] = fmaf(c2, acc[r], sBias2[j]);
         }
       }
     }
+    __syncthreads();  // every wave has read the se rows: the dOut rows move in
+    store_window(sO, wo);
     __syncthreads();
   }
 
@@ -234,10 +242,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (HAS_SE ? 3 : 
       const bool ok = key_ok && (unsigned)dl <= (unsigned)W && nq < N;
       const int j = ok ? dl : 0;
       const float s2 = fmaf(sGain2[j], accS[qb][r],
-                            HAS_SE ? sT[(16 * w + 16 * qb + 4 * g + r) * TS + j] : sBias2[j]);
+                            HAS_SE ? sT[t_at(16 * w + 16 * qb + 4 * g + r, j)] : sBias2[j]);
       const float alpha = ok ? __builtin_amdgcn_exp2f(s2 - lq[4 * qb + r]) : 0.f;
       const float dS = a * alpha * (accU[qb][r] - dq_[4 * qb + r]);
-      wk[r] = sGainC[j] * dS;
+      wk[r] = (HAS_SE ? sGain2[j] * 0.6931471805599453f : sGainC[j]) * dS;
       wv[r] = a * alpha;
     }
     // The weights as bf16 hi + lo pairs, so the products keep their fp32 precision.

@@ -106,7 +106,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
                : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.dout), "s"(p.lse), "s"(p.pos_bias), "s"(p.if_gain),
                  "s"(p.alpha_lr));
   const int lb = xcd_logical_block(blockIdx.x, nblk);
-  const int bh = lb / p.n_chunks, tile = lb - bh * p.n_chunks;
+  const int bh = lb / p.n_chunks, chunk = lb - bh * p.n_chunks;
   const int b = bh / p.H, h = bh - b * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;
   const int NS = NSC > 0 ? NSC : J - W - 1;
@@ -123,24 +123,8 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   bf16_t* dqb = static_cast<bf16_t*>(p.dq) + b * p.dqs.b + h * p.dqs.h;
   const long long rowbase = ((long long)b * p.H + h) * N;
 
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, i = l & 15, g = l >> 4;
-  const int n0 = tile * QT;
-  const int n0w = n0 + 16 * w;
-  const int n = n0w + i;  // query row of this lane's MFMA column
-  const bool row_ok = n < N;
-  // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the
-  // one-hot operand of the long-range dq products must sit there.
-  const bool diag = g == (i >> 2);
-  const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
-  // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
-  int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
-#pragma unroll
-  for (int u = 0; u < CHW; ++u) {
-    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
-    olaneR[u] = opaque(rc_lane<D>(l, u, dosn));
-    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
-    vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
-  }
+
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   int dl_s[NSM];
   load_sparse_deltas(p.taps, dl_s);
 
@@ -177,6 +161,40 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   bf16_t* sKsw = sKs[w];
   float* sTw = reinterpret_cast<float*>(sKsw);
 
+  // The parameter-gradient partials of the workgroup's tiles, summed in tile order.  With
+  // scale_embed a workgroup takes p.tiles_per_block consecutive tiles of its (b,h), so that its
+  // [J x D] dse partial covers that many times 64 queries (the partials are as large as a tile's
+  // dS otherwise); without it one tile.
+  float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
+  f32x4_t accSE[HAS_SE ? TPW : 1];  // this wave's dse^T tiles w, w+4, ...
+#pragma unroll
+  for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
+  const int tpb = HAS_SE ? p.tiles_per_block : 1;
+  for (int tk = 0; tk < tpb; ++tk) {
+  const int tile = chunk * tpb + tk;
+  if (HAS_SE && tile >= p.n_tiles) break;  // one tile per workgroup otherwise: the grid is exact
+  // Lane indices and everything derived from them are formed anew for each tile (from an opaque
+  // copy of the thread index): hoisted out of the tile loop, the per-lane addresses stayed live
+  // across it and spilled.
+  const int l = opaque(tid) & 63, i = l & 15, g = l >> 4;
+  // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the
+  // one-hot operand of the long-range dq products must sit there.
+  const bool diag = g == (i >> 2);
+  const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
+  // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
+  int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
+#pragma unroll
+  for (int u = 0; u < CHW; ++u) {
+    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
+    olaneR[u] = opaque(rc_lane<D>(l, u, dosn));
+    klaneR[u] = opaque(rc_lane<D>(l, u, ksn));
+    vlaneR[u] = opaque(rc_lane<D>(l, u, vsn));
+  }
+  const int n0 = tile * QT;
+  const int n0w = n0 + 16 * w;
+  const int n = n0w + i;  // query row of this lane's MFMA column
+  const bool row_ok = n < N;
+
   // ---- Loads (zero outside [0, N)). ----
   // Dense window K and V rows [n0-32, n0+64), staged once per workgroup in LDS.
   uint4 wk[CWIN], wv[CWIN];
@@ -209,20 +227,20 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   // test was waited for inside the branch, before the long-range loads could be issued.
   const float lse_ld = p.lse[rowbase + (row_ok ? n : N - 1)];
   // The forward's long-range weights of this lane's query ([b,h][tap][query] fp32), on the
-  // diagonal lane (the others read past the buffer and get zeros); one buffer resource per tap
-  // over its [N] row weights, so a row past N reads as zero too.
+  // diagonal lane of a row below N; every other lane's offset lies past the buffer resource (one
+  // over the (b,h)'s NS x N weights, NS N 4 < 2^31 bytes), which returns zeros.  The tap's
+  // offset t N 4 rides in the scalar offset: lanes in range stay in range with it, lanes out of
+  // range stay out.
   float als[NSM];
   {
-    const float* const alb = p.alpha_lr + (long long)bh * NS * N;
-    const unsigned off = diag ? (unsigned)n * 4u : 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.alpha_lr + (long long)bh * NS * N), (short)0, NS * N * 4, 0x00020000);
+    const unsigned off = diag && row_ok ? (unsigned)n * 4u : 0x80000000u;
 #pragma unroll
     for (int t = 0; t < NSM; ++t) {
       als[t] = 0.f;
-      if (NSC > 0 || t < NS) {
-        const __amdgpu_buffer_rsrc_t rA =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(alb + (long long)t * N), (short)0, N * 4, 0x00020000);
-        als[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rA, off, 0, 0));
-      }
+      if (NSC > 0 || t < NS)
+        als[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rA, off, t * N * 4, 0));
     }
   }
   // Long-range rows, one ring of PF slots for both passes: pass 1 takes the V rows of taps
@@ -244,6 +262,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
     sBias2[tid] = bias_ld * kLog2e;
     sGain[tid] = gain_ld;
   }
+  if (tk > 0) __syncthreads();  // the previous tile's reads of the windows and tables are done
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
@@ -373,16 +392,19 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   // dS of every long-range pair, on the query's diagonal lane: into the table (for the SE term,
   // the parameter sums and pass 2) and, with a alpha_j, to launch 2's weights.
   {
-    unsigned* const lw = reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N + n;
+    // One buffer resource over the (b,h)'s NS x N weight dwords: a lane off the diagonal or past
+    // N stores past its end, which the range check drops.
+    const __amdgpu_buffer_rsrc_t rW = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<unsigned*>(p.lrw) + (long long)bh * NS * N, (short)0, NS * N * 4, 0x00020000);
+    const unsigned woff = diag && row_ok ? (unsigned)n * 4u : 0x80000000u;
 #pragma unroll
     for (int t = 0; t < NSM; ++t) {
       if (NSC > 0 || t < NS) {
         const int j = W + 1 + t;
         const float ds = a * als[t] * (uus[t] - Dp);  // zero for masked taps and rows past N
-        if (diag) {
-          sDSw[i * TS + j] = ds;
-          if (row_ok) lw[(long long)t * N] = cvt_pk_bf16(c * sGain[j] * ds, a * als[t]);
-        }
+        if (diag) sDSw[i * TS + j] = ds;
+        __builtin_amdgcn_raw_buffer_store_b32(cvt_pk_bf16(c * sGain[j] * ds, a * als[t]), rW, woff,
+                                              t * N * 4, 0);
       }
     }
   }
@@ -507,7 +529,6 @@ void bwd_dq_mfma_kernel(BwdParams p) {
 
   // dbias / dg column sums of this wave's 16 table rows (its own writes, complete above),
   // and the wave's sum of D' (for da).
-  float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
   if (l < J) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -521,9 +542,6 @@ void bwd_dq_mfma_kernel(BwdParams p) {
     for (int r = 0; r < 16; ++r) acc_if += sDp[w][r];
   }
 
-  f32x4_t accSE[HAS_SE ? TPW : 1];  // this wave's dse^T tiles w, w+4, ...
-#pragma unroll
-  for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
   if constexpr (HAS_SE) {
     __syncthreads();  // all waves' tables and Q rows are complete
     // dse partial on the MFMA: dSE^T (d x j) += Q^T (d x q) dS (q x j) over the tile's 64
@@ -561,6 +579,8 @@ void bwd_dq_mfma_kernel(BwdParams p) {
     }
   }
   if (row_ok && g == 0) p.dpre[rowbase + n] = Dp;
+  }  // tiles
+  const int l = tid & 63, i = l & 15, g = l >> 4;
 
   // The four waves' partial sums meet in their own (now free) table blocks; one partial row per
   // workgroup, summed in wave order.
@@ -621,7 +641,8 @@ static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
 template <int D>
 static hipError_t launch_dq_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
   // The scale_embed variant also serves dse requested at se = 0.
-  if (p.tiles_per_block != 1) return hipErrorInvalidValue;  // one tile per workgroup
+  // Several tiles per workgroup only with scale_embed (its dse partials).
+  if (p.tiles_per_block < 1 || (p.tiles_per_block != 1 && !(p.scale_embed || p.part_se))) return hipErrorInvalidValue;
   if (p.scale_embed || p.part_se) launch_dq_mfma_ns<D, true>(p, nb, st);
   else launch_dq_mfma_ns<D, false>(p, nb, st);
   return hipGetLastError();

@@ -16,8 +16,8 @@ bool fwd_mfma_supported(const FwdParams& p, int D);
 hipError_t launch_fwd_mfma(const FwdParams& p, int D, hipStream_t st);
 
 // Tiling of the backward for these sizes and kernel choice; fills n_tiles / tiles_per_block /
-// n_chunks / n_tiles_kv (one tile per dq workgroup).
-void bwd_plan(BwdParams& p, int D, int dtype);
+// n_chunks / n_tiles_kv (se: scale_embed or its gradient is present).
+void bwd_plan(BwdParams& p, int D, int dtype, bool se);
 
 // bf16 MFMA backward kernels: same conditions as the MFMA forward.
 bool bwd_mfma_supported(const BwdParams& p, int D, int dtype);
