@@ -637,6 +637,28 @@ def time_fwd_bwd(sets, steps, warmup, stream):
     return ms, per, wall
 
 
+def bench_d96(args, dev, stream):
+    """The 85M condU trainer's attention call (train/train_2048_85m_condU.py:54,60-62,169): B8
+    H8 N2048 D96, 44 offsets, same protocol as the headline step; plain, then with scale_embed
+    and IF gain as the trainer's module passes them.  Each with its own fraction of the HBM
+    roofline on its own compulsory step bytes, for comparison with the D = 64 step's."""
+    from dwarf_amd.workloads import TRAINER_D96 as w
+    step_bytes = w.fwd_bytes() + w.bwd_bytes()
+    leg = {"workload": f"B{w.B} H{w.H} N{w.N} D{w.D} J{w.J} bf16 fwd+bwd (85M condU trainer)",
+           "fwd_bwd_algorithmic_bytes": step_bytes}
+    for name, se in (("plain", False), ("scale_embed", True)):
+        sets = make_sets(w, dev, args.sets, scale_embed=se, if_gain=se)
+        ramp(lambda i: run_step(sets, i), args.ramp_ms / 3)
+        ms, per, _ = time_fwd_bwd(sets, args.steps, args.warmup, stream)
+        leg[name] = {"ms_per_step": round(ms, 5), "tok_per_s": round(w.B * w.N / (ms * 1e-3), 1),
+                     "fwd_bwd_frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "kernels": per}
+        print(f"[bench] D=96 leg ({name}) {ms:.4f} ms/step, "
+              f"{leg[name]['fwd_bwd_frac_hbm_peak']:.3f} of HBM peak", file=sys.stderr, flush=True)
+        del sets
+    return leg
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -652,6 +674,7 @@ def main(argv=None):
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-d96-leg", action="store_true", help="skip the D = 96 trainer leg")
     ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
     ap.add_argument("--no-pool", action="store_true", help="skip the interference-pool leg")
     ap.add_argument("--no-generation", action="store_true", help="skip the generation leg")
@@ -752,6 +775,8 @@ def main(argv=None):
             "kernels": se_per}
         print(f"[bench] scale_embed leg {se_ms:.4f} ms/step", file=sys.stderr, flush=True)
         del se_sets
+    if not args.no_d96_leg:
+        result["d96_leg"] = bench_d96(args, dev, stream)
     if not args.no_decode:
         result["decode"] = bench_decode(dev, args.decode_steps)
         print(f"[bench] decode {result['decode']['us_per_step']} us/step over "

@@ -37,7 +37,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : 4)) void bwd_dkdv_mfma_kernel(BwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : 4)) void bwd_dkdv_mfma_kernel(BwdParams p) {
   using G_ = Geo<D>;
   constexpr int KT = 64;                  // key rows per workgroup
   constexpr int KS = G_::KS;
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : 4)) void bwd_d
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range taps in flight: a tap is a few dozen VALU instructions per wave, so the loads
   // run several taps ahead (as many as the register budget of the occupancy target allows).
-  constexpr int PF = (D == 64 && !HAS_SE) ? 3 : 4;
+  constexpr int PF = D > 64 ? 2 : ((D == 64 && !HAS_SE) ? 3 : 4);
   // [query][dense tap] table, row stride 33 (the dense taps): the band's diagonal reads (row
   // 4g + r, tap 4g + r - i) meet at most two to a bank, as with any stride of 33..35, and the
   // table stays small enough for four workgroups per CU.

@@ -37,7 +37,7 @@
 namespace dsqg {
 
 template <int D, bool HAS_SE, int NSC>
-__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3 : 4))) void fwd_mfma_kernel(FwdParams p) {
+__global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3 : 4))) void fwd_mfma_kernel(FwdParams p) {
   using G_ = Geo<D>;
   constexpr int QT = 64;                  // query rows per workgroup
   constexpr int KS = G_::KS;              // 16x16x32 steps over the head dim
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
 #ifdef DSQG_FWD_PF
   constexpr int PF = DSQG_FWD_PF;
 #else
-  constexpr int PF = 3;                   // long-range V blocks held in registers ahead of use
+  constexpr int PF = D > 64 ? 2 : 3;      // long-range V blocks held in registers ahead of use
 #endif
   constexpr int TS = 49;                  // row stride of the per-wave T table (every tap j < 48; odd: rows on distinct banks)
   constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
@@ -64,9 +64,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   // Wave-private staging block (16 rows x RV): the T table (scale_embed), then each long-range
   // tap's V rows, then the output rows.
   __shared__ __align__(16) bf16_t sVs[4][HAS_SE ? XB : 16 * RV];
-  // Per wave: long-range q.k [query][tap].  With scale_embed the scores are added into the T table
-  // instead (its long-range entries are read once, after every tap is scored).
-  __shared__ __align__(16) float sRaw[HAS_SE ? 1 : 4][HAS_SE ? 4 : 16 * TR];
+  // Per wave: long-range q.k [query][tap], in the wave's staging block (free from the band's
+  // query-operand reads to the long-range P V).  With scale_embed the scores are added into the
+  // T table instead (its long-range entries are read once, after every tap is scored).
+  static_assert(16 * TR * 4 <= 16 * RV * 2, "the score table fits the staging block");
   __shared__ float sBias2[kMaxTaps];   // bias * log2(e)
   __shared__ float sGain2[kMaxTaps];   // gain * c * log2(e)
 
@@ -154,9 +155,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
     bias_ld = p.pos_bias[jc * p.H + h];
     gain_ld = p.score_gain ? p.score_gain[h * J + jc] : 1.0f;
   }
-  // The long-range key rows n0w - delta + 0..15 in the row-chunk layout, in two halves (the
-  // second after the dense band has consumed its registers) to bound the register peak.
-  constexpr int NH = (NSM + 1) / 2;
+  // The long-range key rows n0w - delta + 0..15 in the row-chunk layout, in two groups (the
+  // second after the dense band has consumed its registers) to bound the register peak; three
+  // for D > 64, whose rows take four 16-byte pieces per lane (three workgroups per CU then fit).
+  constexpr int NGRP = D > 64 ? 3 : 2;
+  // Group boundaries: taps [0, NH), [NH, NH2), [NH2, NSM).  The first group, live with the window
+  // rows, is the smallest.
+  constexpr int NH = NGRP == 2 ? (NSM + 1) / 2 : (NSM + 3) / 4;
+  constexpr int NH2 = NGRP == 2 ? NSM : NH + (NSM - NH + 1) / 2;
   uint4 kS[NSM][CHW];
 #pragma unroll
   for (int t = 0; t < NH; ++t) {
@@ -234,7 +240,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   // Long-range q.k on the VALU: each lane dots its 16-byte chunk, the CPR lanes of a row sum
   // (DPP), and one lane per row files the score in the wave's [query][tap] table.  The first
   // half's registers are free before the second half is loaded.
-  float* sRw = sRaw[HAS_SE ? 0 : w];
+  float* sRw = reinterpret_cast<float*>(sVs[w]);  // (unused with scale_embed)
   // Score of long-range tap t for each of the wave's rows, less the bias and q.se term
   // (log2 units): gain c log2e q.k, one DPP sum per row.
   auto sparse_score = [&](int t) {
@@ -252,26 +258,34 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
 #pragma unroll
   for (int t = 0; t < NH; ++t)
     if (NSC > 0 || t < NS) sparse_score(t);
+  auto load_k = [&](int t0, int t1) {
 #pragma unroll
-  for (int t = NH; t < NSM; ++t) {
-    if (NSC > 0 || t < NS) {
-      const int m0 = n0w - dl_s[t];
+    for (int t = t0; t < t1; ++t) {
+      if (NSC > 0 || t < NS) {
+        const int m0 = n0w - dl_s[t];
 #pragma unroll
-      for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
+        for (int u = 0; u < CHW; ++u) kS[t][u] = bload16(rK, m0 * ksn + klaneR[u]);
+      }
     }
-  }
+  };
+  load_k(NH, NH2);
   int vlane[CHW];  // this lane's chunks of a wave's 16-row V block (row-chunk layout)
 #pragma unroll
   for (int u = 0; u < CHW; ++u) vlane[u] = opaque(rc_lane<D>(l, u, vsn));
   uint4 vS[PF][CHW];  // long-range V rows n0w - delta + 0..15, PF taps ahead
+  auto prefetch_v = [&]() {
 #pragma unroll
-  for (int t = 0; t < PF; ++t) {
-    if (t < NS) {
-      const int r0 = n0w - dl_s[t];
+    for (int t = 0; t < PF; ++t) {
+      if (t < NS) {
+        const int r0 = n0w - dl_s[t];
 #pragma unroll
-      for (int u = 0; u < CHW; ++u) vS[t][u] = bload16(rV, r0 * vsn + vlane[u]);
+        for (int u = 0; u < CHW; ++u) vS[t][u] = bload16(rV, r0 * vsn + vlane[u]);
+      }
     }
-  }
+  };
+  // With three groups the V rows are requested after the last group is scored (their registers
+  // are the last group's).
+  if constexpr (NGRP == 2) prefetch_v();
 
   __builtin_amdgcn_sched_barrier(0);
 
@@ -291,8 +305,17 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 2 : (NSC != 11 ? 3
   }
 
 #pragma unroll
-  for (int t = NH; t < NSM; ++t)
+  for (int t = NH; t < NH2; ++t)
     if (NSC > 0 || t < NS) sparse_score(t);
+  if constexpr (NGRP == 3) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_k(NH2, NSM);
+#pragma unroll
+    for (int t = NH2; t < NSM; ++t)
+      if (NSC > 0 || t < NS) sparse_score(t);
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch_v();
+  }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the table is written
   __builtin_amdgcn_wave_barrier();
   // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the

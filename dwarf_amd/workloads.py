@@ -11,6 +11,10 @@ the reference's [J,H] layout (kernels/dsqg_attention_v3.py:364), i.e. the transp
   3  B4 H8 N4096 D64, bf16, fwd+bwd, 46 offsets, score gain g[h,j] ~ U(0.5,1.5), IF gain
      a[h] ~ U(0.8,1.2), bias as 0 with linspace(0,2,46).
   4  decode: B256 H12 D64, bf16, 44 offsets, rings of 1537 slots, start positions ~ U[1536,8191].
+
+Not a numbered config: ``TRAINER_D96``, the attention call of the 85M condU trainer
+(train/train_2048_85m_condU.py:54,60-62: batch 8, d_model 768 over 8 heads, i.e. D = 96, N 2048,
+44 offsets), inputs as config 2 with q,k,v ~ N(0,1)/sqrt(96); bench.py's D = 96 leg.
 """
 
 from __future__ import annotations
@@ -63,6 +67,9 @@ WORKLOADS = {
     3: Workload(3, 4, 8, 4096, 64, torch.bfloat16, OFFSETS_J46, True, "condU N=4096 with gains"),
 }
 
+TRAINER_D96 = Workload(5, 8, 8, 2048, 96, torch.bfloat16, OFFSETS_V3, True,
+                       "85M condU trainer's attention (D=96)")
+
 DECODE = dict(index=4, B=256, H=12, D=64, dtype=torch.bfloat16, offsets=OFFSETS_V3, S=1537,
               pos_lo=1536, pos_hi=8191, steps=1000)
 
@@ -76,13 +83,13 @@ def make_inputs(w: Workload, device="cpu", seed: Optional[int] = None):
     """dict of q, k, v, dout, pos_bias, scale_embed, score_gain, if_gain (None when unused)."""
     g = torch.Generator().manual_seed(w.seed if seed is None else seed)
     shp = (w.B, w.H, w.N, w.D)
-    scale = 1.0 / 8.0 if w.index == 2 else 1.0
+    scale = w.D ** -0.5 if w.index in (2, 5) else 1.0
     q = torch.randn(shp, generator=g) * scale
     k = torch.randn(shp, generator=g) * scale
     v = torch.randn(shp, generator=g) * scale
     dout = torch.randn(shp, generator=g)
     J, H = w.J, w.H
-    if w.index == 2:
+    if w.index in (2, 5):
         pos_bias = -3.0 * torch.rand(J, H, generator=g)
     else:
         lin = torch.linspace(0, 2, J)
