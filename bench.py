@@ -489,29 +489,27 @@ def profile_decode(args, dev):
 
 
 def profile_mode(args, w, dev):
-    """Launches one kernel of the workload a few times and a plain copy of known size."""
+    """Launches one kernel of the workload a few times and a plain copy of known size.
+
+    With --profile-sets K > 1 the launches rotate over K input sets (each set's inputs, outputs
+    and workspace about 250 MB at config 2), so a launch's inputs were last touched K - 1
+    launches earlier, with more than the 256 MB Infinity Cache of other data in between: no
+    line of them is cached when it starts, and each L2 miss of a line's first touch is an HBM
+    read."""
     import torch
-    from dwarf_amd import ops
-    from dwarf_amd.workloads import make_inputs
     if args.profile_kernel == "decode":
         return profile_decode(args, dev)
     if args.profile_kernel == "pool":
         return profile_pool(args, dev)
-    if args.profile_se:  # the scale_embed leg's inputs (scale_embed and if_gain)
-        _, d, fl, bl = make_sets(w, dev, 1, scale_embed=True, if_gain=True)[0]
-    else:
-        inp = make_inputs(w, device="cpu", seed=w.seed)
-        d = {k: (None if v is None else v.to(dev)) for k, v in inp.items()}
-        fl = ops.FwdLaunch(d["q"], d["k"], d["v"], d["pos_bias"], d["scale_embed"],
-                           d["score_gain"], d["if_gain"], list(w.offsets))
-        bl = ops.BwdLaunch(d["q"], d["k"], d["v"], d["dout"], fl.lse, d["pos_bias"],
-                           d["scale_embed"], d["score_gain"], d["if_gain"], list(w.offsets),
-                           d["scale_embed"] is not None, d["score_gain"] is not None,
-                           d["if_gain"] is not None, alpha_lr=fl.alpha_lr)
-    fl.run()
-    bl.run()
+    # With --profile-se the scale_embed leg's inputs (scale_embed and if_gain).
+    sets = make_sets(w, dev, max(1, args.profile_sets), scale_embed=args.profile_se,
+                     if_gain=args.profile_se)
+    for _, _, fl, bl in sets:
+        fl.run()
+        bl.run()
     torch.cuda.synchronize()
-    for _ in range(args.profile_reps):
+    for r in range(args.profile_reps):
+        _, _, fl, bl = sets[(r + 1) % len(sets)]
         if args.profile_kernel == "fwd":
             fl.run()
         else:
@@ -684,6 +682,8 @@ def main(argv=None):
                          "FETCH_SIZE / WRITE_SIZE; 'pool': its forward and backward, no copy), "
                          "then exit without a JSON line")
     ap.add_argument("--profile-reps", type=int, default=5)
+    ap.add_argument("--profile-sets", type=int, default=1,
+                    help="with --profile-kernel: input sets the launches rotate over")
     ap.add_argument("--profile-se", action="store_true",
                     help="with --profile-kernel: the scale_embed leg's inputs (scale_embed, if_gain)")
     ap.add_argument("--copy-mib", type=int, default=256)

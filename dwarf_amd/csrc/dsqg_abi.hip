@@ -66,7 +66,7 @@ constexpr size_t kMaxSeSlices = 256;
 
 BwdLayout bwd_layout(const dsqg_bwd_args& a, const BwdParams& p) {
   const dsqg_shape& s = a.shape;
-  const size_t nb = (size_t)s.B * s.H * p.n_chunks;
+  const size_t nb = (size_t)p.n_bgroups * s.H * p.n_chunks;
   BwdLayout L{};
   size_t off = 0;
   L.dpre = off; off = align256(off + sizeof(float) * (size_t)s.B * s.H * s.N);
@@ -114,7 +114,7 @@ int check_bwd(const dsqg_bwd_args* a, BwdParams* p) {
   p->vs = to_strides(a->v_stride); p->dos = to_strides(a->dout_stride);
   bwd_plan(*p, s.D, s.dtype, a->scale_embed != nullptr || a->dscale_embed != nullptr);
   if (s.dtype == DSQG_BF16 && !bwd_mfma_supported(*p, s.D, s.dtype)) return DSQG_EUNSUPPORTED;
-  if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;
+  if ((long long)s.B * s.H * p->n_chunks > INT_MAX / 2) return DSQG_EINVAL;  // >= the partial count
   if ((long long)s.B * s.H * p->n_tiles_kv > INT_MAX / 2) return DSQG_EINVAL;
   return DSQG_OK;
 }
@@ -262,7 +262,7 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream, boo
   const bool rows = (long long)s.B * s.H * s.N > 0;
   ReduceParams r;
   memset(&r, 0, sizeof(r));
-  r.B = s.B; r.H = s.H; r.J = s.J; r.D = s.D;
+  r.B = p.n_bgroups; r.H = s.H; r.J = s.J; r.D = s.D;
   r.n_chunks = rows ? p.n_chunks : 0;  // no rows: the empty sums write zeros
   r.part_bias = p.part_bias; r.part_se = p.part_se;
   r.part_gain = p.part_gain; r.part_if = p.part_if;
@@ -271,7 +271,7 @@ static int run_bwd(const dsqg_bwd_args* a, int phases, dsqg_stream_t stream, boo
   r.se_stage = a->dscale_embed ? reinterpret_cast<float*>(ws + L.se_stage) : nullptr;
   r.se_slices = rows ? L.se_slices : 0;
   r.se_per = L.se_per;
-  const unsigned nb_dq = (unsigned)((long long)s.B * s.H * p.n_chunks);
+  const unsigned nb_dq = (unsigned)((long long)p.n_bgroups * s.H * p.n_chunks);
   const unsigned nb_kv = (unsigned)((long long)s.B * s.H * p.n_tiles_kv);
   if (phases == kPhaseAll && rows) {
     // dq (with the partials), dscale_embed's first stage, then dk/dv with the rest of the

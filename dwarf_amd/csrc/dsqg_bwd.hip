@@ -53,11 +53,16 @@ void bwd_plan(BwdParams& p, int D, int dtype, bool se) {
   p.n_tiles_kv = (p.N + KPB - 1) / KPB;
   // One tile per workgroup: the partial rows (J floats) are small next to a tile's loads, and the
   // single-tile form keeps no per-lane addresses across tiles.  The bf16 dq with scale_embed
-  // takes four consecutive tiles per workgroup instead: its [J x D] fp32 dse partial is as large
-  // as a tile's dS, so one per tile costs as many bytes again as the tile's dq (written, then
-  // read back by the reduction); four tiles per partial cut those bytes to a quarter.
-  p.tiles_per_block = (mfma && se) ? 4 : 1;
-  p.n_chunks = (p.n_tiles + p.tiles_per_block - 1) / p.tiles_per_block;
+  // takes the same head and tile of four batches per workgroup instead: its [J x D] fp32 dse
+  // partial is as large as a tile's dS, so one per tile costs as many bytes again as the tile's
+  // dq (written, then read back by the reduction); one per four tiles cuts them to a quarter.
+  // (Four consecutive tiles of one (b,h) instead put every tile of four times as many (b,h)
+  // slices in flight at once, which overflowed L2: 143 MB more L2-miss reads per launch.)
+  // dse sums over every b and h, dbias / dg / da over b, so a partial may span batches.
+  p.tiles_per_block = 1;
+  p.n_chunks = p.n_tiles;
+  p.batches_per_block = (mfma && se) ? (p.B < 4 ? (p.B > 0 ? p.B : 1) : 4) : 1;
+  p.n_bgroups = (p.B + p.batches_per_block - 1) / p.batches_per_block;
 }
 
 hipError_t launch_bwd_reduce_se_stage(const ReduceParams& r, hipStream_t st) {

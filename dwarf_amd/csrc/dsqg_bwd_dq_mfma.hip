@@ -106,8 +106,9 @@ void bwd_dq_mfma_kernel(BwdParams p) {
                : "s"(p.q), "s"(p.k), "s"(p.v), "s"(p.dout), "s"(p.lse), "s"(p.pos_bias), "s"(p.if_gain),
                  "s"(p.alpha_lr));
   const int lb = xcd_logical_block(blockIdx.x, nblk);
-  const int bh = lb / p.n_chunks, chunk = lb - bh * p.n_chunks;
-  const int b = bh / p.H, h = bh - b * p.H;
+  // Workgroup lb: tile lb % n_chunks of head h of batch group grp ((grp * H + h) * n_chunks + tile).
+  const int gh = lb / p.n_chunks, tile = lb - gh * p.n_chunks;
+  const int grp = gh / p.H, h = gh - grp * p.H;
   const int N = p.N, J = p.taps.J, W = p.taps.W;
   const int NS = NSC > 0 ? NSC : J - W - 1;
   const float c = p.scale, c2 = p.scale * kLog2e;
@@ -116,12 +117,6 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr bool g_grad = DG;
   const int qsn = (int)p.qs.n, ksn = (int)p.ks.n, vsn = (int)p.vs.n, dosn = (int)p.dos.n;
 
-  const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
-  const __amdgpu_buffer_rsrc_t rK = slice_rsrc(static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h, p.ks.n, N, D);
-  const __amdgpu_buffer_rsrc_t rV = slice_rsrc(static_cast<const bf16_t*>(p.v) + b * p.vs.b + h * p.vs.h, p.vs.n, N, D);
-  const __amdgpu_buffer_rsrc_t rO = slice_rsrc(static_cast<const bf16_t*>(p.dout) + b * p.dos.b + h * p.dos.h, p.dos.n, N, D);
-  bf16_t* dqb = static_cast<bf16_t*>(p.dq) + b * p.dqs.b + h * p.dqs.h;
-  const long long rowbase = ((long long)b * p.H + h) * N;
 
 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -161,18 +156,25 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   bf16_t* sKsw = sKs[w];
   float* sTw = reinterpret_cast<float*>(sKsw);
 
-  // The parameter-gradient partials of the workgroup's tiles, summed in tile order.  With
-  // scale_embed a workgroup takes p.tiles_per_block consecutive tiles of its (b,h), so that its
+  // The parameter-gradient partials of the workgroup's (b,h) slices, summed in batch order.  With
+  // scale_embed a workgroup takes its head and tile in p.batches_per_block batches, so that its
   // [J x D] dse partial covers that many times 64 queries (the partials are as large as a tile's
-  // dS otherwise); without it one tile.
+  // dS otherwise); without it one batch.
   float acc_bias = 0.f, acc_gain = 0.f, acc_if = 0.f;
   f32x4_t accSE[HAS_SE ? TPW : 1];  // this wave's dse^T tiles w, w+4, ...
 #pragma unroll
   for (int k = 0; k < (HAS_SE ? TPW : 1); ++k) accSE[k] = zero4();
-  const int tpb = HAS_SE ? p.tiles_per_block : 1;
-  for (int tk = 0; tk < tpb; ++tk) {
-  const int tile = chunk * tpb + tk;
-  if (HAS_SE && tile >= p.n_tiles) break;  // one tile per workgroup otherwise: the grid is exact
+  const int bpb = HAS_SE ? p.batches_per_block : 1;
+  for (int tk = 0; tk < bpb; ++tk) {
+  const int b = grp * bpb + tk;
+  if (HAS_SE && b >= p.B) break;  // one batch per workgroup otherwise: the grid is exact
+  const int bh = b * p.H + h;
+  const __amdgpu_buffer_rsrc_t rQ = slice_rsrc(static_cast<const bf16_t*>(p.q) + b * p.qs.b + h * p.qs.h, p.qs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rK = slice_rsrc(static_cast<const bf16_t*>(p.k) + b * p.ks.b + h * p.ks.h, p.ks.n, N, D);
+  const __amdgpu_buffer_rsrc_t rV = slice_rsrc(static_cast<const bf16_t*>(p.v) + b * p.vs.b + h * p.vs.h, p.vs.n, N, D);
+  const __amdgpu_buffer_rsrc_t rO = slice_rsrc(static_cast<const bf16_t*>(p.dout) + b * p.dos.b + h * p.dos.h, p.dos.n, N, D);
+  bf16_t* dqb = static_cast<bf16_t*>(p.dq) + b * p.dqs.b + h * p.dqs.h;
+  const long long rowbase = ((long long)b * p.H + h) * N;
   // Lane indices and everything derived from them are formed anew for each tile (from an opaque
   // copy of the thread index): hoisted out of the tile loop, the per-lane addresses stayed live
   // across it and spilled.
@@ -262,7 +264,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
     sBias2[tid] = bias_ld * kLog2e;
     sGain[tid] = gain_ld;
   }
-  if (tk > 0) __syncthreads();  // the previous tile's reads of the windows and tables are done
+  if (tk > 0) __syncthreads();  // the previous slice's reads of the windows and tables are done
 #pragma unroll
   for (int u = 0; u < CWIN; ++u) {
     const int ci = tid + u * kBlock;
@@ -642,7 +644,9 @@ template <int D>
 static hipError_t launch_dq_mfma_d(const BwdParams& p, unsigned nb, hipStream_t st) {
   // The scale_embed variant also serves dse requested at se = 0.
   // Several tiles per workgroup only with scale_embed (its dse partials).
-  if (p.tiles_per_block < 1 || (p.tiles_per_block != 1 && !(p.scale_embed || p.part_se))) return hipErrorInvalidValue;
+  if (p.tiles_per_block != 1 || p.batches_per_block < 1 ||
+      (p.batches_per_block != 1 && !(p.scale_embed || p.part_se)))
+    return hipErrorInvalidValue;
   if (p.scale_embed || p.part_se) launch_dq_mfma_ns<D, true>(p, nb, st);
   else launch_dq_mfma_ns<D, false>(p, nb, st);
   return hipGetLastError();

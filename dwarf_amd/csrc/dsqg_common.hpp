@@ -142,7 +142,7 @@ struct FwdParams {
 };
 
 struct ReduceParams {
-  int B, H, J, D, n_chunks;
+  int B, H, J, D, n_chunks;  // B: batch groups of the partials (BwdParams::n_bgroups)
   const float* part_bias; const float* part_se; const float* part_gain; const float* part_if;
   float* dpos_bias; float* dscale_embed; float* dscore_gain; float* dif_gain;
   // dscale_embed is summed in two stages: se_slices runs of se_per consecutive workgroup
@@ -155,6 +155,10 @@ struct BwdParams {
   int n_tiles;          // query tiles per (b,h) of the dq launch
   int tiles_per_block;  // consecutive tiles of one (b,h) handled by one dq workgroup
   int n_chunks;         // dq workgroups per (b,h)
+  // bf16 MFMA dq: batches handled by one workgroup (the same head and tile of each), and the
+  // batch groups that gives; the parameter partials are [n_bgroups * H * n_chunks].
+  int batches_per_block;
+  int n_bgroups;
   int n_tiles_kv;       // key tiles per (b,h) of the dk/dv launch (one workgroup each)
   float scale;
   TapTable taps;
@@ -172,10 +176,10 @@ struct BwdParams {
   void* dk; Strides4 dks;
   void* dv; Strides4 dvs;
   float* dpre;        // workspace [B,H,N]: D' = dOut . o (pre-gain o), fp32
-  float* part_bias;   // workspace [B*H*n_chunks][J]
-  float* part_se;     // workspace [B*H*n_chunks][J][D] or null
-  float* part_gain;   // workspace [B*H*n_chunks][J] or null
-  float* part_if;     // workspace [B*H*n_chunks] or null
+  float* part_bias;   // workspace [n_bgroups*H*n_chunks][J]
+  float* part_se;     // workspace [n_bgroups*H*n_chunks][J][D] or null
+  float* part_gain;   // workspace [n_bgroups*H*n_chunks][J] or null
+  float* part_if;     // workspace [n_bgroups*H*n_chunks] or null
   // bf16 MFMA path: the long-range taps' weights, written by dq and read by dk/dv, workspace
   // [B*H][NS][N] dwords (NS = taps beyond the dense window), for query n and tap W + 1 + t:
   // low half bf16(c g_j dS_j) (the weight of q_n in dk), high half bf16(a alpha_j) (the weight

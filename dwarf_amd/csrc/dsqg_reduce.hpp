@@ -17,7 +17,7 @@ __device__ __forceinline__ float wave_sum_fixed(float x) {
 
 __device__ __forceinline__ void reduce_params_wave(const ReduceParams& r, int t, int lane) {
   const int JH = r.J * r.H;
-  const int per_h = r.B * r.n_chunks;  // partials per head, ordered (b, chunk)
+  const int per_h = r.B * r.n_chunks;  // partials per head, ordered (batch group, chunk)
   if (t < JH) {  // dpos_bias[j,h]
     const int j = t / r.H, h = t - j * r.H;
     float s = 0.f;
