@@ -60,7 +60,9 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
   constexpr int CPRP = G_::CPRP;          // lanes per row in the row-chunk layout
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
-  constexpr int PF = 2;                   // long-range row blocks loaded ahead of use
+  // Long-range row blocks loaded ahead of use: as many as the register budget of the occupancy
+  // target holds without spills (a tap is a few dozen VALU instructions per wave).
+  constexpr int PF = (D > 64 || (HAS_SE && NSC != 11)) ? 2 : (HAS_SE || DG || NSC != 11 ? 3 : 4);
   constexpr int TS = kDqTableStride;
   constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
   constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
