@@ -189,6 +189,21 @@ def test_other_offset_tables_bf16(gpu_device, offsets, N):
     compare(got, ref, "bf16")
 
 
+@pytest.mark.parametrize("D", [80, 96, 128])
+@pytest.mark.parametrize("offsets,N", [(OFFSETS_J47, 2100), (OFFSETS_J46, 1800),
+                                       ((0, 1, 2) + tuple(range(40, 40 + 16 * 37, 37)), 700)])
+def test_other_offset_tables_wide_heads(gpu_device, D, offsets, N):
+    """bf16 with scale_embed, score gain and IF gain over the 47- and 46-offset tables (the
+    kernels specialised for 14 and 13 long-range taps) and a 16-tap table (the generic kernels)
+    at the head dims above 64, whose forward loads its long-range key rows in three bursts and
+    whose kernels keep two long-range taps in flight."""
+    inp = _rand_inputs(1, 2, N, D, offsets, torch.bfloat16, seed=len(offsets) + D)
+    _say(f"bf16 offsets J={len(offsets)} N={N} D={D} with se, g, a")
+    got = gpu_run(inp, offsets, gpu_device)
+    ref = oracle_chunked(inp, offsets, torch.float32)
+    compare(got, ref, "bf16", case=f"J={len(offsets)} D={D} + se, g, a")
+
+
 def test_long_sequence(gpu_device):
     """A sequence of 100,003 tokens (ragged: the last tile holds 35 rows), bf16 with scale_embed
     and the IF gain: row offsets far beyond the workloads' (N * row bytes = 12.8 MB per slice),
