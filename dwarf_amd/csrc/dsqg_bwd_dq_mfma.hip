@@ -181,8 +181,9 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   // copy of the thread index): hoisted out of the tile loop, the per-lane addresses stayed live
   // across it and spilled.
   const int l = opaque(tid) & 63, i = l & 15, g = l >> 4;
-  // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: the
-  // one-hot operand of the long-range dq products must sit there.
+  // The diagonal lane of query i (group i/4, register i%4) owns its long-range taps: it reads
+  // their forward weights, forms their dS and files them in the wave's table, which the row
+  // layout's lanes read for pass 2.
   const bool diag = g == (i >> 2);
   const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
   // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.

@@ -180,29 +180,6 @@ __device__ __forceinline__ void split_bf16x4(float a, float b, float c, float d,
   lo = __builtin_bit_cast(s16x4_t, make_uint2(cvt_pk_bf16(a - ha, b - hb), cvt_pk_bf16(c - hc, d - hd)));
 }
 
-// A bf16 bit pattern (low 16 bits of bits) placed as a one-hot operand at element e.
-__device__ __forceinline__ s16x4_t onehot_bf16_bits(unsigned bits, int e) {
-  return __builtin_bit_cast(s16x4_t, (unsigned long long)bits << (16 * e));
-}
-
-// The split of x placed as a one-hot operand pair at element e (shifts of 16 e bits).
-__device__ __forceinline__ void split_onehot_bf16x4(float x, int e, s16x4_t& hi, s16x4_t& lo) {
-  const __bf16 hb = (__bf16)x;
-  const __bf16 lb = (__bf16)(x - (float)hb);
-  const int sh = 16 * e;
-  hi = __builtin_bit_cast(s16x4_t, (unsigned long long)__builtin_bit_cast(unsigned short, hb) << sh);
-  lo = __builtin_bit_cast(s16x4_t, (unsigned long long)__builtin_bit_cast(unsigned short, lb) << sh);
-}
-
-// The split of x placed as a one-hot operand pair (masks of onehot_masks(e)).
-__device__ __forceinline__ void split_onehot_bf16x4(float x, uint2 m, s16x4_t& hi, s16x4_t& lo) {
-  const unsigned p = cvt_pk_bf16(x, x);
-  const float r = x - __uint_as_float(p << 16);
-  const unsigned q = cvt_pk_bf16(r, r);
-  hi = __builtin_bit_cast(s16x4_t, make_uint2(p & m.x, p & m.y));
-  lo = __builtin_bit_cast(s16x4_t, make_uint2(q & m.x, q & m.y));
-}
-
 // scale_embed [J, D] (fp32, 16-byte aligned) as 48 rows x DP bf16 in LDS (row stride RV; rows
 // >= J and columns >= D zero), optionally with a second plane lo = bf16(se - hi).  The rows come
 // in as 16-byte pieces, loaded into registers first (load) and staged later (store), so a kernel
