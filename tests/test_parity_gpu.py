@@ -204,6 +204,20 @@ def test_other_offset_tables_wide_heads(gpu_device, D, offsets, N):
     compare(got, ref, "bf16", case=f"J={len(offsets)} D={D} + se, g, a")
 
 
+@pytest.mark.parametrize("gains", [True, False])
+@pytest.mark.parametrize("B", [3, 5, 6])
+def test_scale_embed_batch_groups(gpu_device, B, gains):
+    """With scale_embed the dq workgroup takes one head and tile in four batches and sums its
+    parameter partials over them; batch counts that leave a short last group (or one group of
+    three) against the oracle, with the score gain's gradient (the generic dq) and without it
+    (the 11-tap dq of the reference modules' call)."""
+    inp = _rand_inputs(B, 3, 700, 64, OFFSETS_V3, torch.bfloat16, seed=300 + B, gains=gains)
+    _say(f"bf16 B{B} H3 N700 D64 with se, gains={gains} (batch groups)")
+    got = gpu_run(inp, OFFSETS_V3, gpu_device)
+    ref = oracle_chunked(inp, OFFSETS_V3, torch.float32)
+    compare(got, ref, "bf16", case=f"B={B} batch groups + se, gains={gains}")
+
+
 def test_long_sequence(gpu_device):
     """A sequence of 100,003 tokens (ragged: the last tile holds 35 rows), bf16 with scale_embed
     and the IF gain: row offsets far beyond the workloads' (N * row bytes = 12.8 MB per slice),
