@@ -49,11 +49,10 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3
   constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
   constexpr int CHW = G_::CHW;            // chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
-#ifdef DSQG_FWD_PF
-  constexpr int PF = DSQG_FWD_PF;
-#else
-  constexpr int PF = D > 64 ? 2 : 3;      // long-range V blocks held in registers ahead of use
-#endif
+  // Long-range V blocks held in registers ahead of use.  At D > 64 the register peak lies in the
+  // key-row bursts, so four blocks cost no occupancy there (and fewer spills with scale_embed);
+  // at D = 64 a fourth block spills.
+  constexpr int PF = D > 64 ? 4 : 3;
   constexpr int TS = 49;                  // row stride of the per-wave T table (every tap j < 48; odd: rows on distinct banks)
   constexpr int XB = (16 * RV > 32 * TS ? 16 * RV : 32 * TS);  // bf16 elements per staging block
   constexpr int TR = NSM + (NSM & 1);     // row stride of the long-range score table (distinct banks)
