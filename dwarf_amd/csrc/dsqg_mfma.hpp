@@ -102,6 +102,22 @@ __device__ __forceinline__ int rc_chunk(int l, int u) { return (l + 64 * u) % Ge
 template <int D>
 __device__ __forceinline__ bool rc_valid(int l, int u) { return rc_chunk<D>(l, u) < Geo<D>::CPR; }
 
+// Packed row-chunk layout, for row work with no sums across a row (row += w * row): slot
+// s = l + 64u of a 16-row block is chunk s % CPR of row s / CPR, so no lane idles where CPR is
+// not a power of two (D = 96: 3 chunks per lane against the row-chunk layout's 4, of which one
+// in four carries nothing).  For CPR = 4, 8 and 16 it is the row-chunk layout itself.
+template <int D>
+struct Packed {
+  static constexpr int CPR = Geo<D>::CPR;
+  static constexpr int CH = (16 * CPR + 63) / 64;  // chunks per lane of a 16-row block
+};
+template <int D>
+__device__ __forceinline__ int pk_row(int l, int u) { return (l + 64 * u) / Geo<D>::CPR; }
+template <int D>
+__device__ __forceinline__ int pk_chunk(int l, int u) { return (l + 64 * u) % Geo<D>::CPR; }
+template <int D>
+__device__ __forceinline__ bool pk_valid(int l, int u) { return l + 64 * u < 16 * Geo<D>::CPR; }
+
 // An element offset that a slice's buffer resource turns into zeros when added to any row
 // offset a kernel forms: with (N + max offset + 64) * rs * 2 < 2^31 (checked at launch), every
 // row offset r * rs lies in (-2^30, 2^30), so r * rs + kNoElem is past the slice's end.
@@ -112,6 +128,12 @@ constexpr int kNoElem = 1 << 30;
 template <int D>
 __device__ __forceinline__ int rc_lane(int l, int u, int rs) {
   return rc_valid<D>(l, u) ? rc_row<D>(l, u) * rs + rc_chunk<D>(l, u) * 8 : kNoElem;
+}
+
+// The same in the packed layout.
+template <int D>
+__device__ __forceinline__ int pk_lane(int l, int u, int rs) {
+  return pk_valid<D>(l, u) ? pk_row<D>(l, u) * rs + pk_chunk<D>(l, u) * 8 : kNoElem;
 }
 
 // Buffer resource over one (b,h) slice of a [B,H,N,D] bf16 operand: rows [0, N) of row stride rs
