@@ -10,10 +10,10 @@
 //    result layout lane l holds key column l%16 and query rows 4*(l/16)+r, which is exactly the
 //    B operand of dK^T = Q^T (c g dS) and dV^T = dOut^T (a alpha); Q^T and dOut^T come from the
 //    query window [m0, m0+96) in LDS through ds_read_tr16_b64.
-//  * Long-range taps: query rows m0w + delta + 0..15, loaded as whole consecutive rows, D/8
-//    16-byte chunks each, 64 chunks per load in row order (the vector L1 serves that at close to
-//    four times the rate of the MFMA operand order; with no sums across a row, a row need not
-//    start on a power-of-two lane, so at D = 96 every lane carries three chunks).  Their
+//  * Long-range taps: query rows m0w + delta + 0..15, loaded in the row-chunk layout (each
+//    group of four lanes reads 64 contiguous bytes of a row: the vector L1 serves that at close
+//    to four times the rate of the MFMA operand order; at D = 96 every lane carries three
+//    chunks of one row, none idle).  Their
 //    weights come from launch 1, which has every long-range pair's alpha, u and D' in hand
 //    anyway: per (query, tap) the pair (c g_j dS_j, a alpha_j) as two bf16 in one dword, so
 //    this launch computes no long-range score and reads no long-range lse or D'.  A tap adds a
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
   constexpr int CPR = G_::CPR;
   constexpr int CPS = G_::CPS;            // chunks per staged (padded) row
   constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
-  constexpr int CHW = Packed<D>::CH;      // 16-byte chunks per lane of a wave's 16-row block
+  constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range taps in flight: a tap is a few dozen VALU instructions per wave, so the loads
   // run several taps ahead (as many as the register budget of the occupancy target allows).
@@ -120,12 +120,12 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
   int dl_s[NSM];
   load_sparse_deltas(p.taps, dl_s);
   const int klane = opaque(i * ksn + 8 * g), vlane = opaque(i * vsn + 8 * g);
-  // Row-chunk layout (whole rows per D/8 lanes) for the long-range query / dOut rows.
+  // Row-chunk layout for the long-range query / dOut rows.
   int qlaneR[CHW], olaneR[CHW];
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
-    qlaneR[u] = opaque(pk_lane<D>(l, u, qsn));
-    olaneR[u] = opaque(pk_lane<D>(l, u, dosn));
+    qlaneR[u] = opaque(rc_lane<D>(l, u, qsn));
+    olaneR[u] = opaque(rc_lane<D>(l, u, dosn));
   }
 
   // ---- Loads (scale_embed first: the T table waits for it alone). ----
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(lwb + (long long)t * N), (short)0, N * 4, 0x00020000);
 #pragma unroll
     for (int u = 0; u < CHW; ++u)
-      wS[t % PF][u] = __builtin_amdgcn_raw_buffer_load_b32(rW, (unsigned)(m0w + pk_row<D>(l, u) + dl_s[t]) * 4u, 0, 0);
+      wS[t % PF][u] = __builtin_amdgcn_raw_buffer_load_b32(rW, (unsigned)(m0w + rc_row<D>(l, u) + dl_s[t]) * 4u, 0, 0);
   };
 
   if (tid < J) {
@@ -270,8 +270,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
   // ---- Long-range taps: queries m0w + delta + 0..15, one per key row. ----
   // Each tap adds a scaled query / dOut row to each key's dk / dv row (dk_m += c g_j dS q_n,
   // dv_m += a alpha_j dOut_n with n = m + delta_j): no contraction, so it runs on the VALU in
-  // the packed row layout the gathered rows arrive in (slot l + 64u of the 16-row block is
-  // chunk (l + 64u) % (D/8) of row (l + 64u) / (D/8), 8 elements per lane and chunk), as
+  // the row-chunk layout the gathered rows arrive in (8 elements per lane and chunk), as
   // v_dot2_f32_bf16 against (w, 0) and (0, w) (exact products of the bf16 row and bf16 weight,
   // fp32 sums), with no LDS staging and no wait per tap.  The band's MFMA accumulators are first
   // turned into that layout through the wave's share of the (now free) window tiles.
@@ -295,8 +294,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
     if (t < NS) load_tap(t);
   __builtin_amdgcn_sched_barrier(0);
 
-  // MFMA layout (lane (i, g): key i, d = 16 db + 4 g + 0..3) -> packed row layout (lane: key
-  // row pk_row, d = 8 pk_chunk + 0..7), fp32, one matrix at a time through the wave's quarter
+  // MFMA layout (lane (i, g): key i, d = 16 db + 4 g + 0..3) -> row-chunk layout (lane: key
+  // row rc_row, d = 8 rc_chunk + 0..7), fp32, one matrix at a time through the wave's quarter
   // of the window tiles (row stride DP + 4 floats: conflict-free 16-byte writes).
   constexpr int CS = G_::DP + 4;
   static_assert(16 * CS * 4 <= 2 * WIN * RV * 2 / 4, "row-layout staging fits a quarter of the window tiles");
@@ -311,8 +310,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int u = 0; u < CHW; ++u) {
-      const bool ok = pk_valid<D>(l, u);
-      const float* src = cvt + (ok ? pk_row<D>(l, u) * CS + 8 * pk_chunk<D>(l, u) : 0);
+      const bool ok = rc_valid<D>(l, u);
+      const float* src = cvt + (ok ? rc_row<D>(l, u) * CS + 8 * rc_chunk<D>(l, u) : 0);
       const float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
       dst[u][0] = ok ? lo.x : 0.f; dst[u][1] = ok ? lo.y : 0.f; dst[u][2] = ok ? lo.z : 0.f; dst[u][3] = ok ? lo.w : 0.f;
       dst[u][4] = ok ? hi.x : 0.f; dst[u][5] = ok ? hi.y : 0.f; dst[u][6] = ok ? hi.z : 0.f; dst[u][7] = ok ? hi.w : 0.f;
@@ -361,8 +360,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) 
     bf16_t* dvb = static_cast<bf16_t*>(p.dv) + b * p.dvs.b + h * p.dvs.h;
 #pragma unroll
     for (int u = 0; u < CHW; ++u) {
-      const int rr = pk_row<D>(l, u), cc = pk_chunk<D>(l, u);
-      if (pk_valid<D>(l, u) && m0w + rr < N) {
+      const int rr = rc_row<D>(l, u), cc = rc_chunk<D>(l, u);
+      if (rc_valid<D>(l, u) && m0w + rr < N) {
         uint4 kp, vp;
         kp.x = cvt_pk_bf16(kacc[u][0], kacc[u][1]); kp.y = cvt_pk_bf16(kacc[u][2], kacc[u][3]);
         kp.z = cvt_pk_bf16(kacc[u][4], kacc[u][5]); kp.w = cvt_pk_bf16(kacc[u][6], kacc[u][7]);

@@ -7,9 +7,10 @@
 //  1. Dense band (delta = 0..W): keys [n0w-32, n0w+16) as three 16x16 tiles, S^T = K Q^T and
 //     U^T = V dOut^T on the MFMA (v_mfma_f32_16x16x32_bf16), alpha_j from S and lse, u_j = U.
 //  2. Long-range pass 1, V rows only: u_j = dOut . v_j for tap j's 16 value rows n0w - delta + 0..15,
-//     gathered whole-row (D/8 lanes per row) and dotted on the VALU (v_dot2_f32_bf16, DPP sums
-//     over the row's lanes); each row's u goes to the wave's [query][tap] table in LDS without a
-//     wait per tap.  Then D' = sum_j alpha_j u_j (= dOut . o, pre-gain o) is exact (fp32 weights).
+//     gathered in the row-chunk layout (64 contiguous bytes per 4 lanes) and dotted on the VALU
+//     (v_dot2_f32_bf16, DPP sums over the row's lanes); each row's u goes to the wave's
+//     [query][tap] table in LDS without a wait per tap.  Then D' = sum_j alpha_j u_j
+//     (= dOut . o, pre-gain o) is exact (fp32 weights).
 //  3. With D' known, dS_j = a alpha_j (u_j - D') and dq = c sum_j dS_j (g_j k_j + se_j):
 //     the band's part as MFMAs K^T (c g dS)^T with K^T from LDS (ds_read_tr16_b64), whose weights
 //     enter as bf16 hi + lo pairs, so the products keep fp32 weights, as the reference's fp32
@@ -59,6 +60,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
   constexpr int CHW = G_::CHW;            // 16-byte chunks per lane of a wave's 16-row block
   constexpr int CPRP = G_::CPRP;          // lanes per row in the row-chunk layout
+  constexpr int CPL = G_::CPL;            // chunks per lane and row
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range row blocks loaded ahead of use: as many as the register budget of the occupancy
   // target holds without spills (a tap is a few dozen VALU instructions per wave).
@@ -186,7 +188,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   // layout's lanes read for pass 2.
   const bool diag = g == (i >> 2);
   const int qlane = opaque(i * qsn + 8 * g), olane = opaque(i * dosn + 8 * g);
-  // Row-chunk layout (whole rows per D/8 lanes) for the long-range rows and their dot partners.
+  // Row-chunk layout for the long-range rows and their dot partners.
   int qlaneR[CHW], olaneR[CHW], klaneR[CHW], vlaneR[CHW];
 #pragma unroll
   for (int u = 0; u < CHW; ++u) {
@@ -250,7 +252,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   }
   // Long-range rows, one ring of PF slots for both passes: pass 1 takes the V rows of taps
   // 0..NS-1 (slot t % PF), pass 2 the K rows (tap t in slot (NS + t) % PF).  Rows n0w - delta
-  // + 0..15, whole rows per D/8 lanes.
+  // + 0..15, in the row-chunk layout.
   uint4 rS[PF][CHW];
   auto load_rows = [&](int k) {  // k-th block of the combined sequence V(0..NS-1), K(0..NS-1)
     const bool isv = k < NS;
@@ -345,9 +347,12 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   for (int t = 0; t < NSM; ++t) {
     if (NSC > 0 || t < NS) {
 #pragma unroll
-      for (int u = 0; u < CHW; ++u) {
-        const float uv = group_sum<CPRP>(dot8_bf16(oR[u], rS[t % PF][u], 0.f));
-        if (rc_chunk<D>(l, u) == 0) sDSw[rc_row<D>(l, u) * TS + W + 1 + t] = uv;
+      for (int rg = 0; rg < CHW / CPL; ++rg) {
+        float uv = dot8_bf16(oR[rg * CPL], rS[t % PF][rg * CPL], 0.f);
+#pragma unroll
+        for (int pc = 1; pc < CPL; ++pc) uv += dot8_bf16(oR[rg * CPL + pc], rS[t % PF][rg * CPL + pc], 0.f);
+        uv = group_sum<CPRP>(uv);
+        if (l % CPRP == 0) sDSw[rc_row<D>(l, rg * CPL) * TS + W + 1 + t] = uv;
       }
       if (t + PF < 2 * NS) load_rows(t + PF);
     }
@@ -501,9 +506,15 @@ void bwd_dq_mfma_kernel(BwdParams p) {
             xacc[u][2 * e] = fmaf(wc[u], __builtin_bit_cast(float, kw[e] << 16), xacc[u][2 * e]);
             xacc[u][2 * e + 1] = fmaf(wc[u], __builtin_bit_cast(float, kw[e] & 0xffff0000u), xacc[u][2 * e + 1]);
           }
-          if constexpr (DG) {
-            const float qk = group_sum<CPRP>(dot8_bf16(qR[u], kv, 0.f));
-            if (rc_chunk<D>(l, u) == 0) sRAWw[rc_row<D>(l, u) * TS + W + 1 + t] = c * qk;
+        }
+        if constexpr (DG) {
+#pragma unroll
+          for (int rg = 0; rg < CHW / CPL; ++rg) {
+            float qk = dot8_bf16(qR[rg * CPL], rS[slot][rg * CPL], 0.f);
+#pragma unroll
+            for (int pc = 1; pc < CPL; ++pc) qk += dot8_bf16(qR[rg * CPL + pc], rS[slot][rg * CPL + pc], 0.f);
+            qk = group_sum<CPRP>(qk);
+            if (l % CPRP == 0) sRAWw[rc_row<D>(l, rg * CPL) * TS + W + 1 + t] = c * qk;
           }
         }
         // The tap's sums are due here (the empty asm pins them: pure arithmetic is otherwise sunk

@@ -8,7 +8,8 @@
 //     column i = l%16 and keys 4*(l/16) + r of each 16-key block, i.e. delta = n - m is known
 //     per register; taps outside delta in [0, W] (or before row 0) become -inf.
 //  3. Long-range taps: for tap delta the key rows are the contiguous block n0w - delta + 0..15.
-//     They are loaded whole-row (8 lanes x 16 bytes per 128-byte row for D=64) and dotted with
+//     They are loaded in the row-chunk layout (8 lanes x 16 bytes per 128-byte row at D = 64,
+//     4 lanes x 48 bytes per 192-byte row at D = 96) and dotted with
 //     the query rows on the VALU (v_dot2_f32_bf16, DPP sum over the row's lanes); the 16 scores
 //     go through a per-wave LDS table to the lane that owns query i's taps.  An MFMA diagonal
 //     would need the operand order (16 rows x 16 bytes per 16 lanes), which the vector L1
@@ -48,6 +49,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3
   constexpr int CPS = G_::CPS;            // ... per staged row (zero chunks pad D = 80 to 96)
   constexpr int CWIN = (WIN * CPS + kBlock - 1) / kBlock;
   constexpr int CHW = G_::CHW;            // chunks per lane of a wave's 16-row block
+  constexpr int CPL = G_::CPL;            // ... of one row
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range V blocks held in registers ahead of use.  At D > 64 the register peak lies in the
   // key-row bursts, so four blocks cost no occupancy there (and fewer spills with scale_embed);
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3
   // ---- Global loads (all zero-filled outside [0, N) by the buffer range check). ----
   // The query rows go first (the band waits for them): with scale_embed the scale_embed rows
   // and the band's B operand (query rows in the MFMA operand order, for the T table), and in
-  // both variants the query rows in the row-chunk layout (whole rows per D/8 lanes).  Without
+  // both variants the query rows in the row-chunk layout.  Without
   // scale_embed the B operand is read back from that copy, staged in the wave's block after the
   // window barrier (free until the long-range P V), which saves the operand-order global loads
   // (16 rows x 16 B per 16 lanes); with it, the T table needs the operand before the window.
@@ -156,7 +158,8 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3
   }
   // The long-range key rows n0w - delta + 0..15 in the row-chunk layout, in two groups (the
   // second after the dense band has consumed its registers) to bound the register peak; three
-  // for D > 64, whose rows take four 16-byte pieces per lane (three workgroups per CU then fit).
+  // for D > 64, whose rows take three 16-byte pieces per lane where D = 64's take two (in two
+  // groups they spill at three workgroups per CU).
   constexpr int NGRP = D > 64 ? 3 : 2;
   // Group boundaries: taps [0, NH), [NH, NH2), [NH2, NSM).  The first group, live with the window
   // rows, is the smallest.
@@ -236,7 +239,7 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3
       accS[kk] = mfma_16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(kr + 32 * s)), qB[s], accS[kk]);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // Long-range q.k on the VALU: each lane dots its 16-byte chunk, the CPR lanes of a row sum
+  // Long-range q.k on the VALU: each lane dots its 16-byte chunks of a row, the row's lanes sum
   // (DPP), and one lane per row files the score in the wave's [query][tap] table.  The first
   // half's registers are free before the second half is loaded.
   float* sRw = reinterpret_cast<float*>(sVs[w]);  // (unused with scale_embed)
@@ -245,12 +248,14 @@ __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 ? 3 : (NSC != 11 ? 3
   auto sparse_score = [&](int t) {
     const int j = W + 1 + t;
 #pragma unroll
-    for (int u = 0; u < CHW; ++u) {
-      float d = sGain2[j] * dot8_bf16(qR[u], kS[t][u], 0.f);
-      d = group_sum<G_::CPRP>(d);
-      if (rc_chunk<D>(l, u) == 0) {
-        if constexpr (HAS_SE) sTw[rc_row<D>(l, u) * TS + j] += d;
-        else sRw[rc_row<D>(l, u) * TR + t] = d;
+    for (int rg = 0; rg < CHW / CPL; ++rg) {
+      float d = dot8_bf16(qR[rg * CPL], kS[t][rg * CPL], 0.f);
+#pragma unroll
+      for (int pc = 1; pc < CPL; ++pc) d += dot8_bf16(qR[rg * CPL + pc], kS[t][rg * CPL + pc], 0.f);
+      d = group_sum<G_::CPRP>(sGain2[j] * d);
+      if (l % G_::CPRP == 0) {
+        if constexpr (HAS_SE) sTw[rc_row<D>(l, rg * CPL) * TS + j] += d;
+        else sRw[rc_row<D>(l, rg * CPL) * TR + t] = d;
       }
     }
   };

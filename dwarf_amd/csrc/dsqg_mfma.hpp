@@ -74,9 +74,11 @@ __device__ __forceinline__ float dot2_bf16_bits(unsigned a, unsigned b, float ac
 // Head-dim geometry of the bf16 MFMA kernels; D is a multiple of 16 in [32, 128].
 //  * The MFMA K-steps cover DP = D rounded up to 32.  For D = 80 the 16 extra columns are zero
 //    in every operand (loaded as zeros, staged as zeros).
-//  * A row is CPR = D/8 16-byte chunks.  The row-chunk layout (below) spreads a row over CPRP
-//    lanes, CPR rounded up to a power of two, so that DPP sums run over aligned lane groups;
-//    lanes whose chunk is >= CPR carry zeros and store nothing.
+//  * A row is CPR = D/8 16-byte chunks.  The row-chunk layout (below) gives a row CPRP lanes
+//    (a power of two, so that DPP sums run over aligned lane groups) of CPL chunks each: rows of
+//    4, 8 or 16 chunks take that many lanes with one chunk each; rows of 10 or 12 chunks
+//    (D = 80, 96) take four lanes with three chunks each.  Chunks >= CPR carry zeros and store
+//    nothing.
 template <int D>
 struct Geo {
   static_assert(D % 16 == 0 && D >= 32 && D <= 128, "head dim");
@@ -85,38 +87,33 @@ struct Geo {
   static constexpr int DB = D / 16;         // 16-wide head-dim blocks of an output
   static constexpr int CPR = D / 8;         // 16-byte chunks of a row
   static constexpr int CPS = DP / 8;        // ... of a staged (padded) LDS row
-  static constexpr int CPRP = CPR <= 4 ? 4 : (CPR <= 8 ? 8 : 16);
-  static constexpr int CHW = 16 * CPRP / 64;  // chunks per lane of a wave's 16-row block
+  static constexpr int CPRP = (CPR & (CPR - 1)) == 0 ? CPR : 4;  // lanes per row
+  static constexpr int CPL = (CPR + CPRP - 1) / CPRP;          // chunks per lane and row
+  static constexpr int CHW = CPL * 16 * CPRP / 64;  // chunks per lane of a wave's 16-row block
   static constexpr int RV = DP + 8;         // LDS row stride (elements)
 };
 
 // Row-chunk layout of a wave's 16-row block of a [rows][D] bf16 matrix: load u (0 .. CHW-1)
-// gives lane l the 16-byte chunk (l + 64u) % CPRP of row (l + 64u) / CPRP.  Eight (D=64)
-// consecutive lanes then read one whole 128-byte row, which the vector L1 serves at close to
-// four times the rate of the MFMA operand order (16 rows x 16 bytes per 16 lanes), where every
-// group of four lanes touches four different cache lines.
+// gives lane l chunk l % CPRP + CPRP (u % CPL) of row l / CPRP + (64 / CPRP) (u / CPL).  With
+// one chunk per lane and row (CPL = 1) that is chunk (l + 64u) % CPRP of row (l + 64u) / CPRP,
+// eight (D = 64) consecutive lanes reading one whole 128-byte row; at D = 96 load u reads
+// 64-byte piece u of all 16 rows, four lanes each.  Either way each group of four consecutive
+// lanes reads 64 contiguous bytes, which the vector L1 serves at close to four times the rate of
+// the MFMA operand order (16 rows x 16 bytes per 16 lanes), where every group of four lanes
+// touches four different cache lines; on this GPU the D = 96 order gathers 16-row blocks from L2
+// as fast as the D = 64 one, and a fifth faster than 16 lanes per row with four idle.
+// Lane l's CPL loads u = rg CPL .. rg CPL + CPL - 1 are chunks of one row (row group rg): a sum
+// across a row adds those CPL partials in the lane, then the CPRP lanes (group_sum).
 template <int D>
-__device__ __forceinline__ int rc_row(int l, int u) { return (l + 64 * u) / Geo<D>::CPRP; }
+__device__ __forceinline__ int rc_row(int l, int u) {
+  return l / Geo<D>::CPRP + (64 / Geo<D>::CPRP) * (u / Geo<D>::CPL);
+}
 template <int D>
-__device__ __forceinline__ int rc_chunk(int l, int u) { return (l + 64 * u) % Geo<D>::CPRP; }
+__device__ __forceinline__ int rc_chunk(int l, int u) {
+  return l % Geo<D>::CPRP + Geo<D>::CPRP * (u % Geo<D>::CPL);
+}
 template <int D>
 __device__ __forceinline__ bool rc_valid(int l, int u) { return rc_chunk<D>(l, u) < Geo<D>::CPR; }
-
-// Packed row-chunk layout, for row work with no sums across a row (row += w * row): slot
-// s = l + 64u of a 16-row block is chunk s % CPR of row s / CPR, so no lane idles where CPR is
-// not a power of two (D = 96: 3 chunks per lane against the row-chunk layout's 4, of which one
-// in four carries nothing).  For CPR = 4, 8 and 16 it is the row-chunk layout itself.
-template <int D>
-struct Packed {
-  static constexpr int CPR = Geo<D>::CPR;
-  static constexpr int CH = (16 * CPR + 63) / 64;  // chunks per lane of a 16-row block
-};
-template <int D>
-__device__ __forceinline__ int pk_row(int l, int u) { return (l + 64 * u) / Geo<D>::CPR; }
-template <int D>
-__device__ __forceinline__ int pk_chunk(int l, int u) { return (l + 64 * u) % Geo<D>::CPR; }
-template <int D>
-__device__ __forceinline__ bool pk_valid(int l, int u) { return l + 64 * u < 16 * Geo<D>::CPR; }
 
 // An element offset that a slice's buffer resource turns into zeros when added to any row
 // offset a kernel forms: with (N + max offset + 64) * rs * 2 < 2^31 (checked at launch), every
@@ -128,12 +125,6 @@ constexpr int kNoElem = 1 << 30;
 template <int D>
 __device__ __forceinline__ int rc_lane(int l, int u, int rs) {
   return rc_valid<D>(l, u) ? rc_row<D>(l, u) * rs + rc_chunk<D>(l, u) * 8 : kNoElem;
-}
-
-// The same in the packed layout.
-template <int D>
-__device__ __forceinline__ int pk_lane(int l, int u, int rs) {
-  return pk_valid<D>(l, u) ? pk_row<D>(l, u) * rs + pk_chunk<D>(l, u) * 8 : kNoElem;
 }
 
 // Buffer resource over one (b,h) slice of a [B,H,N,D] bf16 operand: rows [0, N) of row stride rs
