@@ -64,7 +64,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range row blocks loaded ahead of use: as many as the register budget of the occupancy
   // target holds without spills (a tap is a few dozen VALU instructions per wave).
-  constexpr int PF = (D > 64 || (HAS_SE && NSC != 11)) ? 2 : (HAS_SE || DG || NSC != 11 ? 3 : 4);
+  constexpr int PF = (D > 64 || (HAS_SE && NSC != 11) || (NSC == 0 && !DG)) ? 2 : (HAS_SE || DG || NSC != 11 ? 3 : 4);
   constexpr int TS = kDqTableStride;
   constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
   constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
@@ -250,20 +250,25 @@ void bwd_dq_mfma_kernel(BwdParams p) {
         als[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rA, off, t * N * 4, 0));
     }
   }
-  // Long-range rows, one ring of PF slots for both passes: pass 1 takes the V rows of taps
-  // 0..NS-1 (slot t % PF), pass 2 the K rows (tap t in slot (NS + t) % PF).  Rows n0w - delta
-  // + 0..15, in the row-chunk layout.
+  // Long-range rows, one ring of PF slots for both passes: block k of the sequence
+  // V(0..NSM-1), K(0..NSM-1) goes to slot k % PF, so pass 1 takes tap t's V rows from slot
+  // t % PF and pass 2 its K rows from slot (NSM + t) % PF.  Every index is a compile-time
+  // constant (the generic-table form, whose tap count NS is known only at run time, skips the
+  // blocks of taps t >= NS instead of shifting the K blocks down): indexed by NS, the ring and
+  // the offsets went to scratch memory.  Rows n0w - delta + 0..15, in the row-chunk layout.
   uint4 rS[PF][CHW];
-  auto load_rows = [&](int k) {  // k-th block of the combined sequence V(0..NS-1), K(0..NS-1)
-    const bool isv = k < NS;
-    const int m0 = n0w - dl_s[isv ? k : k - NS];
+  auto load_rows = [&](int k) {
+    const bool isv = k < NSM;
+    const int t = isv ? k : k - NSM;
+    if (NSC == 0 && t >= NS) return;
+    const int m0 = n0w - dl_s[t];
 #pragma unroll
     for (int u = 0; u < CHW; ++u)
       rS[k % PF][u] = isv ? bload16(rV, m0 * vsn + vlaneR[u]) : bload16(rK, m0 * ksn + klaneR[u]);
   };
 #pragma unroll
   for (int k = 0; k < PF; ++k)
-    if (k < 2 * NS) load_rows(k);
+    if (k < 2 * NSM) load_rows(k);
 
   if (!HAS_SE && tid < J) {
     sBias2[tid] = bias_ld * kLog2e;
@@ -354,8 +359,10 @@ void bwd_dq_mfma_kernel(BwdParams p) {
         uv = group_sum<CPRP>(uv);
         if (l % CPRP == 0) sDSw[rc_row<D>(l, rg * CPL) * TS + W + 1 + t] = uv;
       }
-      if (t + PF < 2 * NS) load_rows(t + PF);
     }
+    // (In the generic-table form the iterations t >= NS consume nothing and issue the first
+    // K blocks of pass 2.)
+    if (t + PF < 2 * NSM) load_rows(t + PF);
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): every row's u is in the table
   __builtin_amdgcn_wave_barrier();
@@ -492,7 +499,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
 #pragma unroll
     for (int t = 0; t < NSM; ++t) {
       if (NSC > 0 || t < NS) {
-        const int slot = (NS + t) % PF;
+        const int slot = (NSM + t) % PF;
         float wc[CHW];
 #pragma unroll
         for (int u = 0; u < CHW; ++u) wc[u] = wnx[u];
@@ -524,7 +531,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) asm volatile("" : "+v"(xacc[u][e]));
         __builtin_amdgcn_sched_barrier(0);
-        if (NS + t + PF < 2 * NS) load_rows(NS + t + PF);
+        if (t + PF < NSM) load_rows(NSM + t + PF);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
