@@ -64,7 +64,7 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range row blocks loaded ahead of use: as many as the register budget of the occupancy
   // target holds without spills (a tap is a few dozen VALU instructions per wave).
-  constexpr int PF = (D > 64 || (HAS_SE && NSC != 11) || (NSC == 0 && !DG)) ? 2 : (HAS_SE || DG || NSC != 11 ? 3 : 4);
+  constexpr int PF = (D > 64 || (HAS_SE && (NSC != 11 || DG)) || (NSC == 0 && !DG)) ? 2 : (HAS_SE || DG || NSC != 11 ? 3 : 4);
   constexpr int TS = kDqTableStride;
   constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
   constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
@@ -648,9 +648,14 @@ void bwd_dq_mfma_kernel(BwdParams p) {
 
 template <int D, bool HAS_SE>
 static void launch_dq_mfma_ns(const BwdParams& p, unsigned nb, hipStream_t st) {
-  if (p.part_gain) {  // the score gain's gradient: the generic-table form with its dg table
+  if (p.part_gain) {  // the score gain's gradient, with its dg table in dynamic LDS
     const size_t dyn = sizeof(float) * 4 * 16 * kDqTableStride;
-    hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0, true>), dim3(nb), dim3(kBlock), dyn, st, p);
+    switch (p.taps.J - p.taps.W - 1) {
+      case 11: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 11, true>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+      case 13: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 13, true>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+      case 14: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 14, true>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+      default: hipLaunchKernelGGL((bwd_dq_mfma_kernel<D, HAS_SE, 0, true>), dim3(nb), dim3(kBlock), dyn, st, p); break;
+    }
     return;
   }
   switch (p.taps.J - p.taps.W - 1) {
