@@ -7,7 +7,8 @@ B8 H12 N2048 D64, bf16, 44 offsets, synthetic seeded inputs already resident in 
 input sets are rotated so that consecutive steps cannot be served from the 256 MB Infinity Cache.
 Prints one JSON line: tok/s (B*N per step), the roofline of the dominant kernel (algorithmic
 bytes per launch over its median launch time, HIP events on the launch stream), the
-fraction of HBM peak for the whole fwd+bwd step, the ring-buffer decode step (workload 4,
+fraction of HBM peak for the whole fwd+bwd step, BASELINE's configs 1 and 3 and the 85M
+trainer's D = 96 call under the same protocol, the ring-buffer decode step (workload 4,
 1000 steps replayed from a HIP graph), the drop-in DSQGAttentionQW layer fwd+bwd, the DWARF
 block's interference pool (causal mean times a sigmoid gate) forward and backward, greedy
 generation with the condU 13M model (incremental vs the reference's full recomputation), and
@@ -657,6 +658,34 @@ def bench_d96(args, dev, stream):
     return leg
 
 
+def bench_configs(args, dev, stream):
+    """BASELINE's other training configurations (its parity cases; the metric is quoted on config
+    2), same protocol as the headline step, each with its own fraction of the HBM roofline on
+    its own compulsory step bytes: config 1 (B8 H8 N2048 D32, the 13M trainers' head dim) and
+    config 3 (B4 H8 N4096 D64, 46 offsets, score gain and IF gain, whose gradients the step
+    requests)."""
+    from dwarf_amd.workloads import WORKLOADS
+    legs = {}
+    for c in (1, 3):
+        w = WORKLOADS[c]
+        step_bytes = w.fwd_bytes() + w.bwd_bytes()
+        sets = make_sets(w, dev, args.sets)
+        ramp(lambda i: run_step(sets, i), args.ramp_ms / 3)
+        ms, per, _ = time_fwd_bwd(sets, args.steps, args.warmup, stream)
+        legs[f"config_{c}"] = {
+            "workload": f"config {c}: B{w.B} H{w.H} N{w.N} D{w.D} J{w.J} bf16 fwd+bwd"
+                        + (" with score gain and IF gain" if c == 3 else ""),
+            "fwd_bwd_algorithmic_bytes": step_bytes, "ms_per_step": round(ms, 5),
+            "tok_per_s": round(w.B * w.N / (ms * 1e-3), 1),
+            "fwd_bwd_frac_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "kernels": per}
+        print(f"[bench] config {c} leg {ms:.4f} ms/step, "
+              f"{legs[f'config_{c}']['fwd_bwd_frac_hbm_peak']:.3f} of HBM peak",
+              file=sys.stderr, flush=True)
+        del sets
+    return legs
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -673,6 +702,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-d96-leg", action="store_true", help="skip the D = 96 trainer leg")
+    ap.add_argument("--no-config-legs", action="store_true",
+                    help="skip the config 1 and config 3 legs")
     ap.add_argument("--no-module", action="store_true", help="skip the drop-in module leg")
     ap.add_argument("--no-pool", action="store_true", help="skip the interference-pool leg")
     ap.add_argument("--no-generation", action="store_true", help="skip the generation leg")
@@ -777,6 +808,8 @@ def main(argv=None):
         del se_sets
     if not args.no_d96_leg:
         result["d96_leg"] = bench_d96(args, dev, stream)
+    if not args.no_config_legs and args.config == 2:
+        result["config_legs"] = bench_configs(args, dev, stream)
     if not args.no_decode:
         result["decode"] = bench_decode(dev, args.decode_steps)
         print(f"[bench] decode {result['decode']['us_per_step']} us/step over "
