@@ -205,19 +205,33 @@ def test_other_offset_tables_wide_heads(gpu_device, D, offsets, N):
 
 
 @pytest.mark.parametrize("gains", [True, False])
-@pytest.mark.parametrize("D", [80, 96, 128])
+@pytest.mark.parametrize("D", [32, 64, 80, 96, 128])
 @pytest.mark.parametrize("offsets", [OFFSETS_V3, OFFSETS_J47], ids=["J44", "J47"])
-def test_wide_heads_without_scale_embed(gpu_device, D, offsets, gains):
-    """bf16 at the head dims above 64 without scale_embed (the 85M trainer's dims with the
-    plain kernels the D = 96 bench leg runs): with the score and IF gains (dq's score-gain
-    gradient on) and without them.  At D = 80 and 96 a row is four lanes of three 16-byte
-    pieces, so each long-range row sum adds three partials in the lane before the lanes'."""
+def test_heads_without_scale_embed(gpu_device, D, offsets, gains):
+    """bf16 without scale_embed at every head dim (the plain kernels, which the headline and the
+    D = 96 bench leg run), with the score and IF gains (dq's score-gain gradient forms for 11
+    and 14 long-range taps) and without them.  At D = 80 and 96 a row is four lanes of three
+    16-byte pieces, so each long-range row sum adds three partials in the lane before the
+    lanes'."""
     inp = _rand_inputs(2, 3, 1300, D, offsets, torch.bfloat16, seed=500 + D + len(offsets),
                        se=False, gains=gains)
     _say(f"bf16 B2 H3 N1300 D{D} J{len(offsets)} no se, gains={gains}")
     got = gpu_run(inp, offsets, gpu_device)
     ref = oracle_chunked(inp, offsets, torch.float32)
     compare(got, ref, "bf16", case=f"D={D} J={len(offsets)} no se, gains={gains}")
+
+
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("offsets", [OFFSETS_J46, OFFSETS_J47], ids=["J46", "J47"])
+def test_score_gain_gradient_with_scale_embed(gpu_device, D, offsets):
+    """scale_embed with both gains over the 46- and 47-offset tables at D = 32 and 64: dq's
+    score-gain gradient forms with scale_embed for 13 and 14 long-range taps (two batches, so
+    a batch group sums two slices)."""
+    inp = _rand_inputs(2, 3, 1100, D, offsets, torch.bfloat16, seed=700 + D + len(offsets))
+    _say(f"bf16 B2 H3 N1100 D{D} J{len(offsets)} with se, g, a")
+    got = gpu_run(inp, offsets, gpu_device)
+    ref = oracle_chunked(inp, offsets, torch.float32)
+    compare(got, ref, "bf16", case=f"D={D} J={len(offsets)} + se, g, a")
 
 
 @pytest.mark.parametrize("gains", [True, False])
