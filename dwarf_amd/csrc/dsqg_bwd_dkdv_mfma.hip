@@ -38,8 +38,9 @@
 
 namespace dsqg {
 
-// Four workgroups per CU (at most 128 VGPRs and 40 KB of LDS each) up to D = 96; three for the
-// scale_embed forms above D = 64, whose se rows and T table take 52 KB of LDS; one at D = 128.
+// Occupancy targets: four workgroups per CU (at most 128 VGPRs and 40 KB of LDS each) up to
+// D = 96; three for the scale_embed forms above D = 64, whose se rows and T table take 52 KB of
+// LDS; none at D = 128 (its registers and LDS set it).
 template <int D, bool HAS_SE, int NSC>
 __global__ __launch_bounds__(kBlock, D == 128 ? 1 : (D > 64 && HAS_SE ? 3 : 4)) void bwd_dkdv_mfma_kernel(BwdParams p) {
   using G_ = Geo<D>;

@@ -63,8 +63,12 @@ void bwd_dq_mfma_kernel(BwdParams p) {
   constexpr int CPL = G_::CPL;            // chunks per lane and row
   constexpr int NSM = NSC > 0 ? NSC : kMaxSparse;
   // Long-range row blocks loaded ahead of use: as many as the register budget of the occupancy
-  // target holds without spills (a tap is a few dozen VALU instructions per wave).
-  constexpr int PF = (D > 64 || (HAS_SE && (NSC != 11 || DG)) || (NSC == 0 && !DG)) ? 2 : (HAS_SE || DG || NSC != 11 ? 3 : 4);
+  // target holds without spills (a tap is a few dozen VALU instructions per wave).  Four in the
+  // plain 11-tap form; two above D = 64, in the scale_embed forms other than the 11-tap one
+  // without the gain's gradient, and in the plain generic-table form; three otherwise.
+  constexpr int PF = (D > 64 || (HAS_SE && (NSC != 11 || DG)) || (NSC == 0 && !DG))
+                         ? 2
+                         : (HAS_SE || DG || NSC != 11 ? 3 : 4);
   constexpr int TS = kDqTableStride;
   constexpr int TST = 38;                 // row stride of the dense-tap T table (2-way bank reads)
   constexpr int KSB = (16 * RV > 32 * TST ? 16 * RV : 32 * TST);  // bf16 per wave staging block
